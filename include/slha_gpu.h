@@ -1,0 +1,140 @@
+/*
+ * slha_gpu.h — additive device-pointer API of the MI355X SLHA v2 library.
+ *
+ * The reference's GPU backend (slhav2-vram) scores one host-resident query
+ * against tiles it uploads itself (GpuScoringPipeline::score_into,
+ * slhav2-vram/src/pipeline.rs:177-230; CudaEngine::score_tiles_on_stream,
+ * slhav2-vram/src/backends/cuda.rs:584-667). This API replaces that pipeline
+ * for callers that keep tiles resident in HBM: every buffer argument named
+ * *_dev is a device pointer, work is enqueued on `stream` (a hipStream_t;
+ * NULL = the default stream) and the call returns without synchronising.
+ * Status codes are those of slha.h plus SLHA_ERR_DEVICE for HIP failures;
+ * the HIP error text goes to the same thread-local slha_last_error_message.
+ */
+#ifndef SLHA_GPU_H
+#define SLHA_GPU_H
+
+#include "slha.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Residual source of a head_dim-128 model. */
+#define SLHA_RESIDUAL_Z 0 /* e = 0: residual bits 0, lambda = sigma = 0 */
+#define SLHA_RESIDUAL_R 1 /* e = key - dequant(tile): the quantisation residual */
+
+/* Element type of key / query arrays. */
+#define SLHA_DTYPE_F32 0
+#define SLHA_DTYPE_BF16 1
+
+/* Score arithmetic. */
+#define SLHA_SCORE_FAST 0  /* reassociated f32 (tolerance 1e-3*(1+|s|)) */
+#define SLHA_SCORE_EXACT 1 /* tile.rs:267-281 order: bit-identical to the scalar path */
+
+/*
+ * Head_dim-128 projection model. The reference builds a model only from a
+ * .slhw file with d > 128 (scirust/src/learned.rs:66, weights.rs:195); its
+ * head_dim-128 benchmark path is the identity latent plus the sign-LSH
+ * projection of scenario.rs:54-114. This constructor builds that model:
+ * Z = 256x128 N(0,1) from SplitMix64(seed) (scenario.rs:59-64), optional RHT
+ * diagonal from SplitMix64(seed ^ 0xA2A2A2A2A2A2A2A2) (learned.rs:158-165).
+ * The handle works with every slha.h entry point taking a model (d = 128).
+ */
+SlhaModel* slha_model_new_raw128(uint64_t seed, int32_t rht, int32_t residual_mode);
+
+/* Copy the model's Z (256*128 floats, row-major) and RHT diagonal (128
+ * floats, may be NULL; all +1 when the model has no RHT) to host memory. */
+int32_t slha_model_projection(const SlhaModel* model, float* z_out, float* rht_diag_out);
+
+/*
+ * Encode keys[n_rows][n_tok][128] (f32 or bf16, device) into
+ * tiles_dev[n_rows][n_tok]. Row r gets head_id = r % n_kv_heads, token t gets
+ * token_id = position = pos0 + t. warm != 0 sets FLAG_WARM. Bit-identical to
+ * the oracle's mode R / mode Z encode (codes, residual bits, sigma, lambda).
+ * Replaces slha_encode_key (slha-c/src/lib.rs:708-752) for batches.
+ */
+int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t key_dtype,
+                        size_t n_rows, size_t n_tok, size_t n_kv_heads, uint32_t pos0,
+                        int32_t codec, int32_t warm, SciRustSlhaTile* tiles_dev, void* stream);
+
+/*
+ * Prepare n_q queries: q_coarse_dev[n_q][128] = q (identity latent) and
+ * q_sign_dev[n_q][4] = sign bits of Z*RHT(q). Replaces slha_prepare_query
+ * (slha-c/src/lib.rs:420-463) for batches.
+ */
+int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int32_t q_dtype,
+                                 size_t n_q, float* q_coarse_dev, uint64_t* q_sign_dev,
+                                 void* stream);
+
+/*
+ * GQA scoring (eq. 2.3, tile.rs:267-281). tiles_dev[n_rows][n_tok] where a
+ * row is one (sequence, KV head); row r serves the `group` query heads
+ * q_*_dev[r*group .. r*group+group). Each tile is read once for the whole
+ * group. scores_dev[r*group + j][t]; hamming_dev (NULL to skip) receives the
+ * per-pair Hamming distance in the same layout. `mode` is SLHA_SCORE_*.
+ * Replaces slha_score_tiles (slha-c/src/lib.rs:527-585) and
+ * GpuScoringPipeline::score_into (slhav2-vram/src/pipeline.rs:177-230).
+ * Tiles are assumed valid (as produced by the encoders); use
+ * slha_gpu_validate_tiles to check caller-supplied bytes.
+ */
+int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
+                       const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
+                       int32_t mode, float* scores_dev, uint32_t* hamming_dev, void* stream);
+
+/*
+ * Validate n tiles on the device (slha-c/src/lib.rs:244-286). status_dev[0]
+ * receives 0, or the lowest failing tile index + 1 (u64); the failing status
+ * (SLHA_ERR_NONFINITE / SLHA_ERR_INVALID_TILE) is status_dev[1].
+ */
+int32_t slha_gpu_validate_tiles(const SciRustSlhaTile* tiles_dev, size_t n, uint64_t* status_dev,
+                                void* stream);
+
+/*
+ * Decode tiles to floats: out_dev[n][128] = dequant_latent (tile.rs:249-255);
+ * with_residual != 0 adds the sign-sketch residual estimate of
+ * LearnedModel::reconstruct_from_tile (learned.rs:288-320) when the model has
+ * no RHT.
+ */
+int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev, size_t n,
+                        int32_t with_residual, float* out_dev, void* stream);
+
+/*
+ * CCOS paged scoring with top-k (ElasticKvCache::score_all, ccos.rs:346-355,
+ * over a paged arena). arena_dev holds pages of page_tiles tiles (a power of
+ * two); page_table_dev[(s*n_kv_heads + h)*max_pages + p] is the physical page
+ * of logical page p of (sequence s, KV head h). seq_len_dev[s] (u32) is the
+ * token count of sequence s and max_len >= every seq_len. Scores of
+ * (s, query head qh = h*group + j, token t) go to
+ * scores_dev[score_base_dev[s] + qh*len(s) + t] (score_base_dev: u64 [n_seq]).
+ * For each (s, qh) the k best tokens (score descending, ties to the lower
+ * token index) go to topk_idx_dev / topk_score_dev[(s*n_kv_heads*group + qh)*k + i];
+ * entries past len(s) are 0xFFFFFFFF / -inf. WARM tiles score coarse-only
+ * (ccos.rs:320-355 via FLAG_WARM). 1 <= k <= 256, or k = 0 to skip top-k.
+ */
+int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_tiles,
+                                  const uint32_t* page_table_dev, size_t max_pages,
+                                  const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
+                                  size_t n_seq, size_t max_len, size_t n_kv_heads, size_t group,
+                                  const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                  float* scores_dev, size_t k, uint32_t* topk_idx_dev,
+                                  float* topk_score_dev, void* stream);
+
+/*
+ * CCOS ladder steps on device-resident tiles (ccos.rs:369-397), applied to
+ * the tiles whose index is listed in slots_dev[n]: op 0 = page_out
+ * (HOT->WARM: residual := 0, lambda := 0, |FLAG_WARM), op 1 = drop_correction
+ * (zero the TQ3/MIX3 correction plane, |FLAG_TQ3_NOCORR; no-op on other
+ * codecs or when already dropped).
+ */
+int32_t slha_gpu_ccos_apply(SciRustSlhaTile* tiles_dev, const uint32_t* slots_dev, size_t n,
+                            int32_t op, void* stream);
+
+/* Synchronise the stream and report any pending HIP error. */
+int32_t slha_gpu_synchronize(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLHA_GPU_H */

@@ -1,0 +1,392 @@
+"""slhav2_amd — MI355X (gfx950) SLHA v2 tile encode + compressed-domain scoring.
+
+Python front of ``libslha.so``, whose C ABI (include/slha.h, include/slha_gpu.h)
+is the drop-in boundary. Everything here is a thin ctypes wrapper: the work is
+done by the HIP kernels inside the library. Importing this package without a
+built ``libslha.so`` raises ImportError; there is no CPU fallback.
+
+Names mirror the reference's C ABI (slha-c/src/lib.rs) and its Rust API
+(scirust::attention::slha_v2): ``score_tiles``, ``encode_key``,
+``prepare_query`` ... Device wrappers take torch tensors that live on the GPU
+(torch is only used for device memory and streams).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+__all__ = [
+    "SlhaError", "Model", "TILE_DTYPE", "lib", "abi_version", "tile_size", "tile_align",
+    "process_tile", "score_tile", "score_tiles", "prepare_query", "encode_key",
+    "decode_latent", "decode_key", "audit", "gpu_encode", "gpu_prepare_queries",
+    "gpu_score", "gpu_validate_tiles", "gpu_decode", "gpu_ccos_apply",
+    "gpu_score_paged_topk",
+]
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libslha.so"
+
+# slha.h status codes / ids
+OK, ERR_NULL, ERR_PANIC, ERR_DIMENSION, ERR_CODEC = 0, -1, -2, -3, -4
+ERR_NONFINITE, ERR_INVALID_TILE, ERR_INVALID_HANDLE, ERR_IO, ERR_UTF8 = -5, -6, -7, -8, -9
+ERR_DEVICE = -10
+CODEC_INT4_SINGLE, CODEC_INT4_GROUPED, CODEC_NF4, CODEC_MIXED, CODEC_TQ3, CODEC_MIX3 = range(6)
+CODEC_NAMES = ["int4", "int4_grouped", "nf4", "mixed", "tq3", "mix3"]
+FLAG_WARM, FLAG_NF4, FLAG_MIXED, FLAG_TQ3, FLAG_TQ3_NOCORR, FLAG_MIX3 = 1, 2, 4, 8, 16, 32
+RESIDUAL_Z, RESIDUAL_R = 0, 1
+DTYPE_F32, DTYPE_BF16 = 0, 1
+SCORE_FAST, SCORE_EXACT = 0, 1
+
+# tile.rs:52-77 — 128-byte tile.
+TILE_DTYPE = np.dtype(
+    {
+        "names": ["latent_kv", "residual_bitmap", "scale", "dynamic_lambda", "residual_sigma",
+                  "token_id", "position", "head_id", "flags", "group_scales"],
+        "formats": [("u1", 64), ("<u8", 4), "<f4", "<f4", "<f4", "<u4", "<u4", "<u2", "<u2",
+                    ("u1", 8)],
+        "offsets": [0, 64, 96, 100, 104, 108, 112, 116, 118, 120],
+        "itemsize": 128,
+    },
+    align=False,
+)
+
+
+class SlhaError(RuntimeError):
+    """A non-zero status from the C ABI, with the thread's last error text."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"SLHA status {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+def _load() -> ctypes.CDLL:
+    # torch ships its own HIP/HSA runtimes (SONAME libamdhip64.so.7) and links
+    # them by the unversioned name, so loading libslha.so first would put two
+    # HIP runtimes in one process. Importing torch first makes libslha.so bind
+    # to the runtime torch already loaded. C callers without torch use the
+    # system runtime alone.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+lib = _load()
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_I32 = ctypes.c_int32
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+
+_SIGS = {
+    "slha_abi_version": (_U32, []),
+    "slha_tile_size": (_SZ, []),
+    "slha_tile_align": (_SZ, []),
+    "slha_last_error_message": (ctypes.c_char_p, []),
+    "slha_clear_error": (None, []),
+    "slha_init": (_P, []),
+    "slha_shutdown": (_I32, [_P]),
+    "slha_process_tile": (_I32, [_P, _P, _P, _P]),
+    "slha_prepare_query": (_I32, [_P, _P, _SZ, _P, _P]),
+    "slha_score_tile": (_I32, [_P, _P, _P, _P, _P]),
+    "slha_score_tiles": (_I32, [_P, _P, _SZ, _P, _P, _P]),
+    "slha_audit": (_P, []),
+    "slha_free_string": (None, [_P]),
+    "slha_weights_load": (_P, [ctypes.c_char_p]),
+    "slha_model_dim": (_SZ, [_P]),
+    "slha_encode_key": (_I32, [_P, _P, _SZ, _U32, _I32, _P]),
+    "slha_decode_latent": (_I32, [_P, _P, _P, _SZ]),
+    "slha_decode_key": (_I32, [_P, _P, _P, _SZ]),
+    "slha_weights_release": (_I32, [_P]),
+    "slha_weights_free": (None, [_P]),
+    "slha_model_new_raw128": (_P, [_U64, _I32, _I32]),
+    "slha_model_projection": (_I32, [_P, _P, _P]),
+    "slha_gpu_encode": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _U32, _I32, _I32, _P, _P]),
+    "slha_gpu_prepare_queries": (_I32, [_P, _P, _I32, _SZ, _P, _P, _P]),
+    "slha_gpu_score": (_I32, [_P, _SZ, _SZ, _P, _P, _SZ, _I32, _P, _P, _P]),
+    "slha_gpu_validate_tiles": (_I32, [_P, _SZ, _P, _P]),
+    "slha_gpu_decode": (_I32, [_P, _P, _SZ, _I32, _P, _P]),
+    "slha_gpu_score_paged_topk": (_I32, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P,
+                                         _P, _SZ, _P, _P, _P]),
+    "slha_gpu_ccos_apply": (_I32, [_P, _P, _SZ, _I32, _P]),
+    "slha_gpu_synchronize": (_I32, [_P]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def last_error() -> str:
+    msg = lib.slha_last_error_message()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def _check(code: int) -> None:
+    if code != OK:
+        raise SlhaError(code, last_error())
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def abi_version() -> int:
+    return int(lib.slha_abi_version())
+
+
+def tile_size() -> int:
+    return int(lib.slha_tile_size())
+
+
+def tile_align() -> int:
+    return int(lib.slha_tile_align())
+
+
+def audit() -> str:
+    p = lib.slha_audit()
+    if not p:
+        raise SlhaError(ERR_PANIC, last_error())
+    try:
+        return ctypes.string_at(p).decode()
+    finally:
+        lib.slha_free_string(p)
+
+
+class Model:
+    """Head_dim-128 projection model (slha_model_new_raw128)."""
+
+    def __init__(self, seed: int = 0, rht: bool = False, residual_mode: int = RESIDUAL_R):
+        h = lib.slha_model_new_raw128(_U64(seed & (2**64 - 1)), int(bool(rht)), residual_mode)
+        if not h:
+            raise SlhaError(ERR_CODEC, last_error())
+        self.handle = h
+        self.seed, self.rht, self.residual_mode = seed, bool(rht), residual_mode
+
+    @property
+    def dim(self) -> int:
+        d = lib.slha_model_dim(self.handle)
+        if d == 0:
+            raise SlhaError(ERR_INVALID_HANDLE, last_error())
+        return int(d)
+
+    def projection(self) -> tuple[np.ndarray, np.ndarray]:
+        z = np.empty((256, 128), np.float32)
+        diag = np.empty(128, np.float32)
+        _check(lib.slha_model_projection(self.handle, _ptr(z), _ptr(diag)))
+        return z, diag
+
+    def release(self) -> None:
+        if self.handle:
+            _check(lib.slha_weights_release(self.handle))
+            self.handle = None
+
+    def __enter__(self) -> "Model":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.release()
+
+
+def _tiles_in(tiles) -> np.ndarray:
+    t = np.ascontiguousarray(tiles)
+    if t.dtype != TILE_DTYPE:
+        t = t.view(TILE_DTYPE) if t.dtype == np.uint8 else t.astype(TILE_DTYPE)
+    return t.reshape(-1)
+
+
+def process_tile(tile, q_coarse, q_sign) -> float:
+    t = _tiles_in(tile)
+    qc = np.ascontiguousarray(q_coarse, np.float32)
+    qs = np.ascontiguousarray(q_sign, np.uint64)
+    out = np.zeros(1, np.float32)
+    _check(lib.slha_process_tile(_ptr(t), _ptr(qc), _ptr(qs), _ptr(out)))
+    return float(out[0])
+
+
+def score_tile(model: Model, tile, q_coarse, q_sign) -> float:
+    t = _tiles_in(tile)
+    qc = np.ascontiguousarray(q_coarse, np.float32)
+    qs = np.ascontiguousarray(q_sign, np.uint64)
+    out = np.zeros(1, np.float32)
+    _check(lib.slha_score_tile(model.handle, _ptr(t), _ptr(qc), _ptr(qs), _ptr(out)))
+    return float(out[0])
+
+
+def score_tiles(model: Model, tiles, q_coarse, q_sign) -> np.ndarray:
+    t = _tiles_in(tiles)
+    qc = np.ascontiguousarray(q_coarse, np.float32)
+    qs = np.ascontiguousarray(q_sign, np.uint64)
+    out = np.zeros(len(t), np.float32)
+    _check(lib.slha_score_tiles(model.handle, _ptr(t), len(t), _ptr(qc), _ptr(qs), _ptr(out)))
+    return out
+
+
+def prepare_query(model: Model, q) -> tuple[np.ndarray, np.ndarray]:
+    qv = np.ascontiguousarray(q, np.float32)
+    qc = np.zeros(128, np.float32)
+    qs = np.zeros(4, np.uint64)
+    _check(lib.slha_prepare_query(model.handle, _ptr(qv), qv.size, _ptr(qc), _ptr(qs)))
+    return qc, qs
+
+
+def encode_key(model: Model, key, position: int, codec: int) -> np.ndarray:
+    k = np.ascontiguousarray(key, np.float32)
+    out = np.zeros(1, TILE_DTYPE)
+    _check(lib.slha_encode_key(model.handle, _ptr(k), k.size, position, codec, _ptr(out)))
+    return out[0]
+
+
+def decode_latent(model: Model, tile) -> np.ndarray:
+    t = _tiles_in(tile)
+    out = np.zeros(128, np.float32)
+    _check(lib.slha_decode_latent(model.handle, _ptr(t), _ptr(out), 128))
+    return out
+
+
+def decode_key(model: Model, tile) -> np.ndarray:
+    t = _tiles_in(tile)
+    out = np.zeros(128, np.float32)
+    _check(lib.slha_decode_key(model.handle, _ptr(t), _ptr(out), 128))
+    return out
+
+
+# --------------------------------------------------------------------------
+# Device API (torch tensors on the GPU)
+
+def _stream(stream=None) -> int:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _dev_ptr(t) -> int:
+    if t is None:
+        return 0
+    if not t.is_cuda:
+        raise ValueError("device API expects GPU tensors")
+    if not t.is_contiguous():
+        raise ValueError("device API expects contiguous tensors")
+    return int(t.data_ptr())
+
+
+def gpu_encode(model: Model, keys, codec: int, n_kv_heads: int = 1, pos0: int = 0,
+               warm: bool = False, out=None, stream=None):
+    """keys: [n_rows, n_tok, 128] (or [n_tok, 128]) f32/bf16 -> tiles uint8 [n_rows, n_tok, 128]."""
+    import torch
+
+    k = keys if keys.dim() == 3 else keys.unsqueeze(0)
+    n_rows, n_tok, d = k.shape
+    if d != 128:
+        raise ValueError("keys must have 128 features")
+    dtype = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}[k.dtype]
+    if out is None:
+        out = torch.empty((n_rows, n_tok, 128), dtype=torch.uint8, device=k.device)
+    _check(lib.slha_gpu_encode(model.handle, _dev_ptr(k), dtype, n_rows, n_tok, n_kv_heads, pos0,
+                               codec, int(bool(warm)), _dev_ptr(out), _stream(stream)))
+    return out if keys.dim() == 3 else out[0]
+
+
+def gpu_prepare_queries(model: Model, q, stream=None):
+    """q: [n, 128] f32/bf16 -> (q_coarse f32 [n,128], q_sign int64 [n,4] (u64 bits))."""
+    import torch
+
+    qq = q.reshape(-1, 128)
+    dtype = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}[qq.dtype]
+    qc = torch.empty((qq.shape[0], 128), dtype=torch.float32, device=qq.device)
+    qs = torch.empty((qq.shape[0], 4), dtype=torch.int64, device=qq.device)
+    _check(lib.slha_gpu_prepare_queries(model.handle, _dev_ptr(qq), dtype, qq.shape[0],
+                                        _dev_ptr(qc), _dev_ptr(qs), _stream(stream)))
+    return qc, qs
+
+
+def gpu_score(tiles, q_coarse, q_sign, group: int = 1, mode: int = SCORE_FAST,
+              hamming: bool = False, out=None, stream=None):
+    """tiles uint8 [n_rows, n_tok, 128]; q_* [n_rows*group, ...] -> scores f32 [n_rows*group, n_tok]."""
+    import torch
+
+    t = tiles if tiles.dim() == 3 else tiles.unsqueeze(0)
+    n_rows, n_tok, _ = t.shape
+    if q_coarse.shape[0] != n_rows * group or q_sign.shape[0] != n_rows * group:
+        raise ValueError("expected n_rows*group queries")
+    if out is None:
+        out = torch.empty((n_rows * group, n_tok), dtype=torch.float32, device=t.device)
+    ham = torch.empty((n_rows * group, n_tok), dtype=torch.int32, device=t.device) if hamming else None
+    _check(lib.slha_gpu_score(_dev_ptr(t), n_rows, n_tok, _dev_ptr(q_coarse), _dev_ptr(q_sign),
+                              group, mode, _dev_ptr(out), _dev_ptr(ham), _stream(stream)))
+    return (out, ham) if hamming else out
+
+
+def gpu_validate_tiles(tiles, stream=None):
+    """Returns (index, status) of the lowest invalid tile, or None."""
+    import torch
+
+    t = tiles.reshape(-1, 128)
+    st = torch.empty(1, dtype=torch.int64, device=t.device)
+    _check(lib.slha_gpu_validate_tiles(_dev_ptr(t), t.shape[0], _dev_ptr(st), _stream(stream)))
+    v = int(st.cpu().numpy().view(np.uint64)[0])
+    if v == 2**64 - 1:
+        return None
+    return (v >> 8) - 1, -(v & 0xFF)
+
+
+def gpu_decode(model: Model, tiles, with_residual: bool = False, stream=None):
+    import torch
+
+    t = tiles.reshape(-1, 128)
+    out = torch.empty((t.shape[0], 128), dtype=torch.float32, device=t.device)
+    _check(lib.slha_gpu_decode(model.handle, _dev_ptr(t), t.shape[0], int(bool(with_residual)),
+                               _dev_ptr(out), _stream(stream)))
+    return out
+
+
+def gpu_ccos_apply(tiles, slots, op: int, stream=None) -> None:
+    """op 0 = page_out (HOT->WARM), op 1 = drop_correction; slots int32 tensor of tile indices."""
+    t = tiles.reshape(-1, 128)
+    _check(lib.slha_gpu_ccos_apply(_dev_ptr(t), _dev_ptr(slots), slots.numel(), op,
+                                   _stream(stream)))
+
+
+def gpu_score_paged_topk(arena, page_tiles: int, page_table, max_pages: int, seq_len,
+                         n_kv_heads: int, group: int, q_coarse, q_sign, k: int,
+                         max_len: int | None = None, scores=None, stream=None):
+    """Paged CCOS scoring + top-k. seq_len: int32 GPU tensor [n_seq].
+
+    Returns (scores f32 flat, topk_idx int32 [n_seq, Hq, k], topk_val f32 [n_seq, Hq, k]);
+    scores of sequence s start at score_base[s] = Hq * sum(seq_len[:s]).
+    """
+    import torch
+
+    n_seq = seq_len.numel()
+    hq = n_kv_heads * group
+    lens64 = seq_len.to(torch.int64)
+    base = torch.zeros(n_seq, dtype=torch.int64, device=seq_len.device)
+    if n_seq > 1:
+        base[1:] = torch.cumsum(lens64, 0)[:-1] * hq
+    if max_len is None:
+        max_len = int(lens64.max().item()) if n_seq else 0
+    if scores is None:
+        total = int(lens64.sum().item()) * hq
+        scores = torch.empty(max(total, 1), dtype=torch.float32, device=seq_len.device)
+    idx = torch.empty((n_seq, hq, max(k, 1)), dtype=torch.int32, device=seq_len.device)
+    val = torch.empty((n_seq, hq, max(k, 1)), dtype=torch.float32, device=seq_len.device)
+    _check(lib.slha_gpu_score_paged_topk(
+        _dev_ptr(arena), page_tiles, _dev_ptr(page_table), max_pages, _dev_ptr(seq_len),
+        _dev_ptr(base), n_seq, max_len, n_kv_heads, group, _dev_ptr(q_coarse), _dev_ptr(q_sign),
+        _dev_ptr(scores), k, _dev_ptr(idx), _dev_ptr(val), _stream(stream)))
+    return scores, idx, val
+
+
+def synchronize(stream=None) -> None:
+    _check(lib.slha_gpu_synchronize(_stream(stream)))

@@ -1,0 +1,89 @@
+"""Build libslha.so (HIP, gfx950) and the CPU oracle library.
+
+No cmake/ninja: one hipcc link line for the product library and one gcc line
+per oracle library. Everything is written in-tree so the built files travel
+with the repository snapshot to the GPU box.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libslha.so"
+ORACLE = ROOT / "oracle"
+ORACLE_LIB = ORACLE / "liboracle_slha.so"
+CPU_BASELINE_LIB = ORACLE / "libcpu_baseline.so"
+
+ARCH = os.environ.get("SLHA_GPU_ARCH", "gfx950")
+
+HIP_SOURCES = ["slha_kernels.hip", "slha_abi.cpp"]
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Rust never contracts a*b+c; exact kernels rely on this. Fast kernels
+    # call fmaf() explicitly.
+    "-ffp-contract=off",
+    # Keep hipcc away from packed-FP32 instructions.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: cannot build libslha.so")
+
+
+def _run(cmd: list[str], cwd: Path) -> None:
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, cwd=cwd, check=True)
+
+
+def build_library(verbose: bool = True) -> Path:
+    srcs = [str(CSRC / s) for s in HIP_SOURCES]
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
+    _run(cmd, CSRC)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    cc = shutil.which("gcc") or "cc"
+    common = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+              "-Wall", "-Wextra"]
+    _run([cc, *common, "slha_oracle.c", "-lm", "-o", ORACLE_LIB.name], ORACLE)
+    # The CPU baseline (AVX-512/AVX2 restatement of simd.rs) is runtime
+    # dispatched, so it builds without host-specific -march flags.
+    _run([cc, "-O3", "-std=c11", "-fPIC", "-shared", "-Wall", "-pthread", "-ffp-contract=off",
+          "cpu_baseline.c",
+          "slha_oracle.c", "-lm", "-o", CPU_BASELINE_LIB.name], ORACLE)
+    return ORACLE_LIB
+
+
+def build_all() -> None:
+    build_oracle()
+    build_library()
+
+
+if __name__ == "__main__":
+    what = sys.argv[1] if len(sys.argv) > 1 else "all"
+    if what == "oracle":
+        build_oracle()
+    elif what == "lib":
+        build_library()
+    else:
+        build_all()

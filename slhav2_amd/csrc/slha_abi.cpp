@@ -1,0 +1,798 @@
+// slha_abi.cpp — the C ABI of libslha.so (include/slha.h + include/slha_gpu.h).
+//
+// Boundary semantics follow slha-c/src/lib.rs:
+//   * every call clears the thread-local last error and runs under a panic
+//     barrier (C++ exceptions -> SLHA_ERR_PANIC, lib.rs:91-105);
+//   * outputs are written only after every check passed;
+//   * model handles are opaque tokens in a process-wide registry; released
+//     tokens are quarantined so a stale pointer never aliases a live model
+//     (lib.rs:124-205).
+// All compute runs on the GPU: host-pointer entry points stage their buffers
+// through per-thread device memory on a per-thread stream.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <shared_mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/slha.h"
+#include "../../include/slha_gpu.h"
+#include "slha_launch.h"
+
+using namespace slha;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Errors (lib.rs:35-105)
+
+constexpr size_t kErrCap = 512;
+thread_local char g_last_error[kErrCap] = {0};
+
+void clear_error() { g_last_error[0] = 0; }
+
+void set_error(const std::string& m) {
+    const size_t n = m.size() < kErrCap - 1 ? m.size() : kErrCap - 1;
+    std::memcpy(g_last_error, m.data(), n);
+    g_last_error[n] = 0;
+}
+
+struct SlhaError {
+    int32_t code;
+    std::string msg;
+};
+
+[[noreturn]] void fail(int32_t code, const char* fmt, ...) {
+    char buf[kErrCap];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw SlhaError{code, buf};
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(SLHA_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+template <class F>
+int32_t ffi_status(F&& body) {
+    clear_error();
+    try {
+        body();
+        return SLHA_OK;
+    } catch (const SlhaError& e) {
+        set_error(e.msg);
+        return e.code;
+    } catch (...) {
+        set_error("panic caught at the SLHA C ABI boundary");
+        return SLHA_ERR_PANIC;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Context (lib.rs:107-122, 331-360)
+
+struct ContextObj {
+    uint32_t abi_version;
+    uint32_t reserved;
+};
+ContextObj g_context = {SLHA_ABI_VERSION, 0};
+
+// ---------------------------------------------------------------------------
+// Product-side SplitMix64 / Box–Muller generator (rng.rs:7-52) for Z and the
+// RHT diagonal of head_dim-128 models.
+
+struct Rng {
+    uint64_t state;
+    explicit Rng(uint64_t seed) : state(seed ^ 0x9E3779B97F4A7C15ull) {}
+    uint64_t next_u64() {
+        state += 0x9E3779B97F4A7C15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    float next_unit() { return (float)(next_u64() >> 40) * (1.0f / 16777216.0f); }
+    float next_gaussian() {
+        const float u1 = std::fmax(next_unit(), 1.0e-7f);
+        const float u2 = next_unit();
+        const float r = std::sqrt(-2.0f * std::log(u1));
+        return r * std::cos(2.0f * 3.14159265358979323846f * u2);
+    }
+};
+
+const float kPi = 3.14159265358979323846f;
+float lambda_c() { return std::sqrt(kPi / (2.0f * 256.0f)); }  // scenario.rs:30-32
+float rht_inv() { return 1.0f / std::sqrt(128.0f); }            // incoherence.rs:66
+float sqrt_half_pi() { return std::sqrt(kPi / 2.0f); }          // learned.rs:303
+
+// ---------------------------------------------------------------------------
+// Models
+
+struct Model {
+    size_t d = 128;
+    uint64_t seed = 0;
+    bool rht = false;
+    int residual_mode = kResidualR;
+    std::vector<float> z;     // [256][128]
+    std::vector<float> diag;  // [128], +-1
+    std::mutex mu;
+    std::unordered_map<int, std::pair<float*, float*>> dev;
+
+    ~Model() {
+        for (auto& kv : dev) {
+            int cur = 0;
+            if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(kv.first) == hipSuccess) {
+                (void)hipFree(kv.second.first);
+                (void)hipFree(kv.second.second);
+                (void)hipSetDevice(cur);
+            }
+        }
+    }
+
+    // Device copies of (Z, diag-or-null) on the current device.
+    std::pair<const float*, const float*> device_buffers() {
+        int device = 0;
+        check_hip(hipGetDevice(&device), "hipGetDevice");
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = dev.find(device);
+        if (it == dev.end()) {
+            float* zd = nullptr;
+            float* dd = nullptr;
+            check_hip(hipMalloc(&zd, z.size() * sizeof(float)), "hipMalloc(Z)");
+            check_hip(hipMemcpy(zd, z.data(), z.size() * sizeof(float), hipMemcpyHostToDevice),
+                      "hipMemcpy(Z)");
+            if (rht) {
+                check_hip(hipMalloc(&dd, diag.size() * sizeof(float)), "hipMalloc(diag)");
+                check_hip(hipMemcpy(dd, diag.data(), diag.size() * sizeof(float),
+                                    hipMemcpyHostToDevice),
+                          "hipMemcpy(diag)");
+            }
+            it = dev.emplace(device, std::make_pair(zd, dd)).first;
+        }
+        return {it->second.first, it->second.second};
+    }
+};
+
+}  // namespace
+
+struct SlhaModel {
+    uint64_t opaque;
+};
+struct SlhaContext {
+    ContextObj obj;
+};
+
+namespace {
+
+struct Registry {
+    std::shared_mutex mu;
+    std::unordered_map<uintptr_t, std::pair<std::unique_ptr<SlhaModel>, std::shared_ptr<Model>>> live;
+    std::vector<std::unique_ptr<SlhaModel>> retired;
+};
+
+Registry& registry() {
+    static Registry* r = new Registry();  // never destroyed: handles outlive static teardown
+    return *r;
+}
+
+SlhaModel* register_model(std::shared_ptr<Model> m) {
+    auto token = std::make_unique<SlhaModel>();
+    token->opaque = 0;
+    SlhaModel* p = token.get();
+    auto& r = registry();
+    std::unique_lock<std::shared_mutex> lock(r.mu);
+    r.live.emplace(reinterpret_cast<uintptr_t>(p), std::make_pair(std::move(token), std::move(m)));
+    return p;
+}
+
+std::shared_ptr<Model> model_of(const SlhaModel* model) {  // lib.rs:170-194
+    if (!model) fail(SLHA_ERR_NULL, "model handle is NULL");
+    if (reinterpret_cast<uintptr_t>(model) % alignof(SlhaModel) != 0)
+        fail(SLHA_ERR_INVALID_HANDLE, "model handle is misaligned");
+    auto& r = registry();
+    std::shared_lock<std::shared_mutex> lock(r.mu);
+    auto it = r.live.find(reinterpret_cast<uintptr_t>(model));
+    if (it == r.live.end()) fail(SLHA_ERR_INVALID_HANDLE, "model handle is not a live SLHA handle");
+    return it->second.second;
+}
+
+// ---------------------------------------------------------------------------
+// Validation (lib.rs:233-286)
+
+void validate_finite(const float* v, size_t n, const char* name) {
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(v[i])) fail(SLHA_ERR_NONFINITE, "%s[%zu] is not finite", name, i);
+}
+
+void validate_tile(const SciRustSlhaTile& t) {
+    const uint16_t known = SLHA_FLAG_WARM | SLHA_FLAG_NF4 | SLHA_FLAG_MIXED | SLHA_FLAG_TQ3 |
+                           SLHA_FLAG_TQ3_NOCORR | SLHA_FLAG_MIX3;
+    const uint16_t codecs = SLHA_FLAG_NF4 | SLHA_FLAG_MIXED | SLHA_FLAG_TQ3 | SLHA_FLAG_MIX3;
+    if (t.flags & (uint16_t)~known)
+        fail(SLHA_ERR_INVALID_TILE, "tile contains unknown flag bits: 0x%04x", t.flags);
+    if (__builtin_popcount(t.flags & codecs) > 1)
+        fail(SLHA_ERR_INVALID_TILE, "tile selects more than one latent codec");
+    if ((t.flags & SLHA_FLAG_TQ3_NOCORR) && !(t.flags & (SLHA_FLAG_TQ3 | SLHA_FLAG_MIX3)))
+        fail(SLHA_ERR_INVALID_TILE, "correction-drop flag requires the TQ3 or MIX3 codec");
+    if (!std::isfinite(t.scale) || !std::isfinite(t.dynamic_lambda) ||
+        !std::isfinite(t.residual_sigma))
+        fail(SLHA_ERR_NONFINITE, "tile metadata contains a non-finite float");
+    if (t.scale < 0.0f || t.dynamic_lambda < 0.0f || t.residual_sigma < 0.0f)
+        fail(SLHA_ERR_INVALID_TILE,
+             "tile scale, dynamic lambda, and residual sigma must be non-negative");
+}
+
+SciRustSlhaTile read_tile(const SciRustSlhaTile* p) {  // unaligned-safe read
+    SciRustSlhaTile t;
+    std::memcpy(&t, p, sizeof t);
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// Per-thread device staging for host-pointer entry points
+
+struct Staging {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    void* buf = nullptr;
+    size_t cap = 0;
+};
+thread_local Staging g_staging;
+
+void require_device() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        fail(SLHA_ERR_DEVICE, "no HIP device is available to the SLHA library");
+}
+
+// Returns a device buffer of at least `bytes` bytes and the thread's stream.
+char* staging(size_t bytes, hipStream_t* stream) {
+    require_device();
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    Staging& s = g_staging;
+    if (s.device != device) {
+        s.device = device;
+        s.stream = nullptr;
+        s.buf = nullptr;
+        s.cap = 0;
+        check_hip(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "hipStreamCreate");
+    }
+    if (s.cap < bytes) {
+        if (s.buf) check_hip(hipFree(s.buf), "hipFree(staging)");
+        s.buf = nullptr;
+        s.cap = 0;
+        const size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes;
+        check_hip(hipMalloc(&s.buf, cap), "hipMalloc(staging)");
+        s.cap = cap;
+    }
+    *stream = s.stream;
+    return static_cast<char*>(s.buf);
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// GPU eq. 2.3 (exact order) over host tiles; scores written to host `out`.
+void score_host_tiles(const SciRustSlhaTile* tiles, size_t n, const float* qc, const uint64_t* qs,
+                      float* out) {
+    const size_t tb = align256(n * sizeof(SciRustSlhaTile));
+    const size_t qb = align256(128 * sizeof(float) + 4 * sizeof(uint64_t));
+    hipStream_t s;
+    char* base = staging(tb + qb + align256(n * sizeof(float)), &s);
+    char* td = base;
+    float* qcd = reinterpret_cast<float*>(base + tb);
+    uint64_t* qsd = reinterpret_cast<uint64_t*>(base + tb + 128 * sizeof(float));
+    float* sd = reinterpret_cast<float*>(base + tb + qb);
+    check_hip(hipMemcpyAsync(td, tiles, n * sizeof(SciRustSlhaTile), hipMemcpyHostToDevice, s), "H2D tiles");
+    check_hip(hipMemcpyAsync(qcd, qc, 128 * sizeof(float), hipMemcpyHostToDevice, s), "H2D q_coarse");
+    check_hip(hipMemcpyAsync(qsd, qs, 4 * sizeof(uint64_t), hipMemcpyHostToDevice, s), "H2D q_sign");
+    check_hip(launch_score_rows(td, 1, (uint32_t)n, 1, qcd, qsd, true, sd, nullptr, s), "score kernel");
+    check_hip(hipMemcpyAsync(out, sd, n * sizeof(float), hipMemcpyDeviceToHost, s), "D2H scores");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+std::string json_escape(const char* s) {
+    std::string o;
+    for (; *s; ++s) {
+        if (*s == '"' || *s == '\\') o.push_back('\\');
+        if ((unsigned char)*s >= 0x20) o.push_back(*s);
+    }
+    return o;
+}
+
+}  // namespace
+
+// ===========================================================================
+// slha.h
+
+extern "C" {
+
+uint32_t slha_abi_version(void) { return SLHA_ABI_VERSION; }
+size_t slha_tile_size(void) { return sizeof(SciRustSlhaTile); }
+size_t slha_tile_align(void) { return alignof(SciRustSlhaTile); }
+
+const char* slha_last_error_message(void) { return g_last_error; }
+void slha_clear_error(void) { clear_error(); }
+
+SlhaContext* slha_init(void) {
+    clear_error();
+    return reinterpret_cast<SlhaContext*>(&g_context);
+}
+
+int32_t slha_shutdown(SlhaContext* context) {
+    clear_error();
+    if (!context) return SLHA_OK;
+    if (context != reinterpret_cast<SlhaContext*>(&g_context)) {
+        set_error("context handle was not returned by slha_init");
+        return SLHA_ERR_INVALID_HANDLE;
+    }
+    return SLHA_OK;
+}
+
+int32_t slha_process_tile(const SciRustSlhaTile* tile, const float* q_coarse,
+                          const uint64_t* q_sign, float* score_out) {
+    return ffi_status([&] {
+        if (!tile || !q_coarse || !q_sign || !score_out)
+            fail(SLHA_ERR_NULL, "slha_process_tile received a NULL pointer");
+        const SciRustSlhaTile t = read_tile(tile);
+        float qc[128];
+        uint64_t qs[4];
+        std::memcpy(qc, q_coarse, sizeof qc);
+        std::memcpy(qs, q_sign, sizeof qs);
+        validate_tile(t);
+        validate_finite(qc, 128, "q_coarse");
+        float score = 0.0f;
+        score_host_tiles(&t, 1, qc, qs, &score);
+        if (!std::isfinite(score))
+            fail(SLHA_ERR_NONFINITE, "tile scoring produced a non-finite result");
+        std::memcpy(score_out, &score, sizeof score);
+    });
+}
+
+int32_t slha_prepare_query(const SlhaModel* model, const float* q, size_t d, float* q_coarse,
+                           uint64_t* q_sign) {
+    return ffi_status([&] {
+        if (!q || !q_coarse || !q_sign)
+            fail(SLHA_ERR_NULL, "slha_prepare_query received a NULL data pointer");
+        auto m = model_of(model);
+        if (d != m->d)
+            fail(SLHA_ERR_DIMENSION, "query dimension mismatch: received %zu, expected %zu", d, m->d);
+        std::vector<float> qv(d);
+        std::memcpy(qv.data(), q, d * sizeof(float));
+        validate_finite(qv.data(), d, "q");
+        auto zb = m->device_buffers();
+        hipStream_t s;
+        char* base = staging(align256(512) + align256(512) + align256(32), &s);
+        float* qd = reinterpret_cast<float*>(base);
+        float* qcd = reinterpret_cast<float*>(base + 512);
+        uint64_t* qsd = reinterpret_cast<uint64_t*>(base + 1024);
+        check_hip(hipMemcpyAsync(qd, qv.data(), 512, hipMemcpyHostToDevice, s), "H2D q");
+        check_hip(launch_prepare_queries(qd, kDtypeF32, 1, zb.first, zb.second, rht_inv(), qcd, qsd, s),
+                  "prepare kernel");
+        float qc[128];
+        uint64_t qs[4];
+        check_hip(hipMemcpyAsync(qc, qcd, sizeof qc, hipMemcpyDeviceToHost, s), "D2H q_coarse");
+        check_hip(hipMemcpyAsync(qs, qsd, sizeof qs, hipMemcpyDeviceToHost, s), "D2H q_sign");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        validate_finite(qc, 128, "q_coarse");
+        std::memcpy(q_coarse, qc, sizeof qc);
+        std::memcpy(q_sign, qs, sizeof qs);
+    });
+}
+
+int32_t slha_score_tile(const SlhaModel* model, const SciRustSlhaTile* tile, const float* q_coarse,
+                        const uint64_t* q_sign, float* score_out) {
+    return ffi_status([&] {
+        if (!tile || !q_coarse || !q_sign || !score_out)
+            fail(SLHA_ERR_NULL, "slha_score_tile received a NULL pointer");
+        (void)model_of(model);
+        const SciRustSlhaTile t = read_tile(tile);
+        float qc[128];
+        uint64_t qs[4];
+        std::memcpy(qc, q_coarse, sizeof qc);
+        std::memcpy(qs, q_sign, sizeof qs);
+        validate_tile(t);
+        validate_finite(qc, 128, "q_coarse");
+        float score = 0.0f;
+        score_host_tiles(&t, 1, qc, qs, &score);
+        if (!std::isfinite(score))
+            fail(SLHA_ERR_NONFINITE, "tile scoring produced a non-finite result");
+        std::memcpy(score_out, &score, sizeof score);
+    });
+}
+
+int32_t slha_score_tiles(const SlhaModel* model, const SciRustSlhaTile* tiles, size_t n_tiles,
+                         const float* q_coarse, const uint64_t* q_sign, float* scores_out) {
+    return ffi_status([&] {
+        if (!tiles || !q_coarse || !q_sign || !scores_out)
+            fail(SLHA_ERR_NULL, "slha_score_tiles received a NULL pointer");
+        (void)model_of(model);
+        const size_t kMaxTiles = size_t(1) << 20;  // lib.rs:207-208
+        if (n_tiles > kMaxTiles)
+            fail(SLHA_ERR_DIMENSION, "n_tiles=%zu exceeds the safety bound %zu", n_tiles, kMaxTiles);
+        if (n_tiles == 0) return;
+        float qc[128];
+        uint64_t qs[4];
+        std::memcpy(qc, q_coarse, sizeof qc);
+        std::memcpy(qs, q_sign, sizeof qs);
+        validate_finite(qc, 128, "q_coarse");
+        std::vector<SciRustSlhaTile> tv(n_tiles);
+        std::memcpy(tv.data(), tiles, n_tiles * sizeof(SciRustSlhaTile));
+        for (size_t i = 0; i < n_tiles; ++i) validate_tile(tv[i]);
+        std::vector<float> sv(n_tiles);
+        score_host_tiles(tv.data(), n_tiles, qc, qs, sv.data());
+        for (size_t i = 0; i < n_tiles; ++i)
+            if (!std::isfinite(sv[i]))
+                fail(SLHA_ERR_NONFINITE, "tile %zu scoring produced a non-finite result", i);
+        std::memcpy(scores_out, sv.data(), n_tiles * sizeof(float));
+    });
+}
+
+char* slha_audit(void) {
+    clear_error();
+    try {
+        std::string j = "{\"abi_version\":" + std::to_string(SLHA_ABI_VERSION) +
+                        ",\"tile_size\":" + std::to_string(sizeof(SciRustSlhaTile)) +
+                        ",\"tile_align\":" + std::to_string(alignof(SciRustSlhaTile)) +
+                        ",\"layout_ok\":true";
+        int n = 0;
+        if (hipGetDeviceCount(&n) == hipSuccess && n > 0) {
+            int dev = 0;
+            hipDeviceProp_t prop;
+            if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+                j += ",\"device\":\"" + json_escape(prop.name) + "\",\"arch\":\"" +
+                     json_escape(prop.gcnArchName) + "\"";
+            // Known answer (scirust/examples/basic_usage.rs:9-45): a ramp
+            // (i-64)/16 quantised with codec INT4_SINGLE, lambda 0.5,
+            // q0 = q1 = 1, q_sign = 0x123456789ABCDEF0 x4 scores exactly -8.
+            std::shared_ptr<Model> m = std::make_shared<Model>();
+            m->z.assign(256 * 128, 0.0f);
+            m->diag.assign(128, 1.0f);
+            float key[128];
+            for (int i = 0; i < 128; ++i) key[i] = ((float)i - 64.0f) / 16.0f;
+            hipStream_t s;
+            char* base = staging(4096, &s);
+            check_hip(hipMemcpyAsync(base, key, sizeof key, hipMemcpyHostToDevice, s), "H2D key");
+            auto zb = m->device_buffers();
+            check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, 0, kCodecInt4Single, kResidualZ, 0,
+                                    zb.first, nullptr, lambda_c(), rht_inv(), base + 1024, s),
+                      "encode kernel");
+            SciRustSlhaTile t;
+            check_hip(hipMemcpyAsync(&t, base + 1024, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
+            check_hip(hipStreamSynchronize(s), "sync");
+            t.dynamic_lambda = 0.5f;
+            float qc[128] = {0};
+            qc[0] = qc[1] = 1.0f;
+            uint64_t qs[4] = {0x123456789ABCDEF0ull, 0x123456789ABCDEF0ull, 0x123456789ABCDEF0ull,
+                              0x123456789ABCDEF0ull};
+            float score = 0.0f;
+            score_host_tiles(&t, 1, qc, qs, &score);
+            char buf[64];
+            std::snprintf(buf, sizeof buf, "%.6f", (double)score);
+            j += std::string(",\"kat_basic_usage\":") + buf + ",\"ok\":" + (score == -8.0f ? "true" : "false");
+        } else {
+            j += ",\"device\":null,\"ok\":false";
+        }
+        j += "}";
+        char* out = static_cast<char*>(std::malloc(j.size() + 1));
+        if (!out) return nullptr;
+        std::memcpy(out, j.c_str(), j.size() + 1);
+        return out;
+    } catch (const SlhaError& e) {
+        set_error(e.msg);
+        return nullptr;
+    } catch (...) {
+        set_error("panic caught while running the SLHA self-audit");
+        return nullptr;
+    }
+}
+
+void slha_free_string(char* string) { std::free(string); }
+
+SlhaModel* slha_weights_load(const char* path) {
+    clear_error();
+    if (!path) {
+        set_error("weights path is NULL");
+        return nullptr;
+    }
+    // Reject invalid UTF-8 like CStr::to_str (lib.rs:658-661).
+    const unsigned char* p = reinterpret_cast<const unsigned char*>(path);
+    while (*p) {
+        int extra = (*p < 0x80) ? 0 : ((*p >> 5) == 0x6) ? 1 : ((*p >> 4) == 0xE) ? 2 : ((*p >> 3) == 0x1E) ? 3 : -1;
+        if (extra < 0) {
+            set_error("weights path is not valid UTF-8");
+            return nullptr;
+        }
+        ++p;
+        for (int i = 0; i < extra; ++i, ++p)
+            if ((*p & 0xC0) != 0x80) {
+                set_error("weights path is not valid UTF-8");
+                return nullptr;
+            }
+    }
+    set_error(std::string("cannot load '") + path +
+              "': .slhw learned projections (d > 128) are not supported by this build; "
+              "use slha_model_new_raw128 for head_dim-128 keys");
+    return nullptr;
+}
+
+size_t slha_model_dim(const SlhaModel* model) {
+    size_t d = 0;
+    const int32_t rc = ffi_status([&] { d = model_of(model)->d; });
+    return rc == SLHA_OK ? d : 0;
+}
+
+int32_t slha_encode_key(const SlhaModel* model, const float* key, size_t d, uint32_t position,
+                        int32_t codec, SciRustSlhaTile* out_tile) {
+    return ffi_status([&] {
+        if (!key || !out_tile) fail(SLHA_ERR_NULL, "slha_encode_key received a NULL data pointer");
+        auto m = model_of(model);
+        if (d != m->d)
+            fail(SLHA_ERR_DIMENSION, "key dimension mismatch: received %zu, expected %zu", d, m->d);
+        if (codec < 0 || codec > 5)
+            fail(SLHA_ERR_CODEC, "unknown codec id %d; expected an integer from 0 to 5", codec);
+        std::vector<float> kv(d);
+        std::memcpy(kv.data(), key, d * sizeof(float));
+        validate_finite(kv.data(), d, "key");
+        auto zb = m->device_buffers();
+        hipStream_t s;
+        char* base = staging(1024, &s);
+        check_hip(hipMemcpyAsync(base, kv.data(), 512, hipMemcpyHostToDevice, s), "H2D key");
+        check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, position, codec, m->residual_mode, 0,
+                                zb.first, zb.second, lambda_c(), rht_inv(), base + 512, s),
+                  "encode kernel");
+        SciRustSlhaTile t;
+        check_hip(hipMemcpyAsync(&t, base + 512, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        validate_tile(t);
+        std::memcpy(out_tile, &t, sizeof t);
+    });
+}
+
+static int32_t decode_common(const SlhaModel* model, const SciRustSlhaTile* tile, float* out,
+                             size_t d, bool with_residual, const char* fn) {
+    return ffi_status([&] {
+        if (!tile || !out) fail(SLHA_ERR_NULL, "%s received a NULL data pointer", fn);
+        auto m = model_of(model);
+        if (d != m->d)
+            fail(SLHA_ERR_DIMENSION, "output dimension mismatch: received %zu, expected %zu", d, m->d);
+        const SciRustSlhaTile t = read_tile(tile);
+        validate_tile(t);
+        auto zb = m->device_buffers();
+        hipStream_t s;
+        char* base = staging(1024, &s);
+        check_hip(hipMemcpyAsync(base, &t, sizeof t, hipMemcpyHostToDevice, s), "H2D tile");
+        const float* z = (with_residual && !m->rht) ? zb.first : nullptr;
+        check_hip(launch_decode(base, 1, z, sqrt_half_pi(), reinterpret_cast<float*>(base + 512), s),
+                  "decode kernel");
+        float v[128];
+        check_hip(hipMemcpyAsync(v, base + 512, sizeof v, hipMemcpyDeviceToHost, s), "D2H");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        validate_finite(v, 128, with_residual ? "reconstruction" : "dequantized_latent");
+        std::memcpy(out, v, sizeof v);
+    });
+}
+
+int32_t slha_decode_latent(const SlhaModel* model, const SciRustSlhaTile* tile, float* out,
+                           size_t d) {
+    return decode_common(model, tile, out, d, false, "slha_decode_latent");
+}
+
+int32_t slha_decode_key(const SlhaModel* model, const SciRustSlhaTile* tile, float* out, size_t d) {
+    return decode_common(model, tile, out, d, true, "slha_decode_key");
+}
+
+int32_t slha_weights_release(SlhaModel* model) {
+    if (!model) {
+        clear_error();
+        return SLHA_OK;
+    }
+    return ffi_status([&] {
+        if (reinterpret_cast<uintptr_t>(model) % alignof(SlhaModel) != 0)
+            fail(SLHA_ERR_INVALID_HANDLE, "model handle is misaligned");
+        auto& r = registry();
+        std::shared_ptr<Model> victim;
+        {
+            std::unique_lock<std::shared_mutex> lock(r.mu);
+            auto it = r.live.find(reinterpret_cast<uintptr_t>(model));
+            if (it == r.live.end())
+                fail(SLHA_ERR_INVALID_HANDLE, "model handle is not a live SLHA handle");
+            r.retired.push_back(std::move(it->second.first));
+            victim = std::move(it->second.second);
+            r.live.erase(it);
+        }
+    });
+}
+
+void slha_weights_free(SlhaModel* model) { (void)slha_weights_release(model); }
+
+// ===========================================================================
+// slha_gpu.h
+
+SlhaModel* slha_model_new_raw128(uint64_t seed, int32_t rht, int32_t residual_mode) {
+    SlhaModel* out = nullptr;
+    const int32_t rc = ffi_status([&] {
+        if (residual_mode != SLHA_RESIDUAL_Z && residual_mode != SLHA_RESIDUAL_R)
+            fail(SLHA_ERR_CODEC, "unknown residual mode %d", residual_mode);
+        auto m = std::make_shared<Model>();
+        m->seed = seed;
+        m->rht = rht != 0;
+        m->residual_mode = residual_mode;
+        m->diag.assign(128, 1.0f);
+        if (m->rht) {  // learned.rs:158-165, incoherence.rs:89-98
+            Rng r(seed ^ 0xA2A2A2A2A2A2A2A2ull);
+            for (auto& x : m->diag) x = r.next_unit() < 0.5f ? -1.0f : 1.0f;
+        }
+        m->z.resize(256 * 128);  // scenario.rs:59-64
+        Rng r(seed);
+        for (auto& x : m->z) x = r.next_gaussian();
+        out = register_model(std::move(m));
+    });
+    return rc == SLHA_OK ? out : nullptr;
+}
+
+int32_t slha_model_projection(const SlhaModel* model, float* z_out, float* rht_diag_out) {
+    return ffi_status([&] {
+        if (!z_out) fail(SLHA_ERR_NULL, "z_out is NULL");
+        auto m = model_of(model);
+        std::memcpy(z_out, m->z.data(), m->z.size() * sizeof(float));
+        if (rht_diag_out) std::memcpy(rht_diag_out, m->diag.data(), m->diag.size() * sizeof(float));
+    });
+}
+
+int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t key_dtype,
+                        size_t n_rows, size_t n_tok, size_t n_kv_heads, uint32_t pos0,
+                        int32_t codec, int32_t warm, SciRustSlhaTile* tiles_dev, void* stream) {
+    return ffi_status([&] {
+        auto m = model_of(model);
+        if (codec < 0 || codec > 5)
+            fail(SLHA_ERR_CODEC, "unknown codec id %d; expected an integer from 0 to 5", codec);
+        if (key_dtype != SLHA_DTYPE_F32 && key_dtype != SLHA_DTYPE_BF16)
+            fail(SLHA_ERR_DIMENSION, "unknown key dtype %d", key_dtype);
+        if (n_kv_heads == 0 || n_kv_heads > 65536)
+            fail(SLHA_ERR_DIMENSION, "n_kv_heads=%zu out of range", n_kv_heads);
+        if (n_tok > 0xFFFFFFFFull || n_rows * n_tok >= (1ull << 40))
+            fail(SLHA_ERR_DIMENSION, "batch too large: %zu rows x %zu tokens", n_rows, n_tok);
+        const uint64_t n = (uint64_t)n_rows * n_tok;
+        if (n == 0) return;
+        if (!keys_dev || !tiles_dev) fail(SLHA_ERR_NULL, "slha_gpu_encode received a NULL pointer");
+        require_device();
+        auto zb = m->device_buffers();
+        check_hip(launch_encode(keys_dev, key_dtype, n, (uint32_t)n_tok, (uint32_t)n_kv_heads, pos0,
+                                codec, m->residual_mode, warm, zb.first, zb.second, lambda_c(),
+                                rht_inv(), tiles_dev, static_cast<hipStream_t>(stream)),
+                  "encode kernel");
+    });
+}
+
+int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int32_t q_dtype,
+                                 size_t n_q, float* q_coarse_dev, uint64_t* q_sign_dev,
+                                 void* stream) {
+    return ffi_status([&] {
+        auto m = model_of(model);
+        if (q_dtype != SLHA_DTYPE_F32 && q_dtype != SLHA_DTYPE_BF16)
+            fail(SLHA_ERR_DIMENSION, "unknown query dtype %d", q_dtype);
+        if (n_q == 0) return;
+        if (!q_dev || !q_coarse_dev || !q_sign_dev)
+            fail(SLHA_ERR_NULL, "slha_gpu_prepare_queries received a NULL pointer");
+        require_device();
+        auto zb = m->device_buffers();
+        check_hip(launch_prepare_queries(q_dev, q_dtype, n_q, zb.first, zb.second, rht_inv(),
+                                         q_coarse_dev, q_sign_dev, static_cast<hipStream_t>(stream)),
+                  "prepare kernel");
+    });
+}
+
+int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
+                       const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
+                       int32_t mode, float* scores_dev, uint32_t* hamming_dev, void* stream) {
+    return ffi_status([&] {
+        if (mode != SLHA_SCORE_FAST && mode != SLHA_SCORE_EXACT)
+            fail(SLHA_ERR_DIMENSION, "unknown score mode %d", mode);
+        if (group == 0 || group > kMaxGroup)
+            fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
+        if (n_rows > 65535 || n_tok > 0xFFFFFFFFull)
+            fail(SLHA_ERR_DIMENSION, "n_rows=%zu / n_tok=%zu out of range", n_rows, n_tok);
+        if (n_rows == 0 || n_tok == 0) return;
+        if (!tiles_dev || !q_coarse_dev || !q_sign_dev || !scores_dev)
+            fail(SLHA_ERR_NULL, "slha_gpu_score received a NULL pointer");
+        require_device();
+        check_hip(launch_score_rows(tiles_dev, (uint32_t)n_rows, (uint32_t)n_tok, (uint32_t)group,
+                                    q_coarse_dev, q_sign_dev, mode == SLHA_SCORE_EXACT, scores_dev,
+                                    hamming_dev, static_cast<hipStream_t>(stream)),
+                  "score kernel");
+    });
+}
+
+int32_t slha_gpu_validate_tiles(const SciRustSlhaTile* tiles_dev, size_t n, uint64_t* status_dev,
+                                void* stream) {
+    return ffi_status([&] {
+        if (!status_dev) fail(SLHA_ERR_NULL, "status_dev is NULL");
+        if (n > 0 && !tiles_dev) fail(SLHA_ERR_NULL, "tiles_dev is NULL");
+        require_device();
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        check_hip(launch_fill_u64(status_dev, 1, ~0ull, s), "fill kernel");
+        check_hip(launch_validate(tiles_dev, n, status_dev, s), "validate kernel");
+    });
+}
+
+int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev, size_t n,
+                        int32_t with_residual, float* out_dev, void* stream) {
+    return ffi_status([&] {
+        auto m = model_of(model);
+        if (n == 0) return;
+        if (!tiles_dev || !out_dev) fail(SLHA_ERR_NULL, "slha_gpu_decode received a NULL pointer");
+        require_device();
+        auto zb = m->device_buffers();
+        const float* z = (with_residual && !m->rht) ? zb.first : nullptr;
+        check_hip(launch_decode(tiles_dev, n, z, sqrt_half_pi(), out_dev,
+                                static_cast<hipStream_t>(stream)),
+                  "decode kernel");
+    });
+}
+
+int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_tiles,
+                                  const uint32_t* page_table_dev, size_t max_pages,
+                                  const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
+                                  size_t n_seq, size_t max_len, size_t n_kv_heads, size_t group,
+                                  const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                  float* scores_dev, size_t k, uint32_t* topk_idx_dev,
+                                  float* topk_score_dev, void* stream) {
+    return ffi_status([&] {
+        if (page_tiles == 0 || (page_tiles & (page_tiles - 1)) != 0 || page_tiles > (1u << 30))
+            fail(SLHA_ERR_DIMENSION, "page_tiles=%zu must be a power of two", page_tiles);
+        if (group == 0 || group > kMaxGroup)
+            fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
+        if (k > kMaxTopK) fail(SLHA_ERR_DIMENSION, "k=%zu exceeds %u", k, kMaxTopK);
+        if (n_kv_heads == 0 || n_seq * n_kv_heads > 65535 || max_len > 0xFFFFFFFFull ||
+            max_pages > 0xFFFFFFFFull || (uint64_t)max_len > (uint64_t)max_pages * page_tiles)
+            fail(SLHA_ERR_DIMENSION, "paged geometry out of range (n_seq=%zu n_kv=%zu max_len=%zu)",
+                 n_seq, n_kv_heads, max_len);
+        if (n_seq == 0 || max_len == 0) return;
+        if (!arena_dev || !page_table_dev || !seq_len_dev || !score_base_dev || !q_coarse_dev ||
+            !q_sign_dev || !scores_dev || (k > 0 && (!topk_idx_dev || !topk_score_dev)))
+            fail(SLHA_ERR_NULL, "slha_gpu_score_paged_topk received a NULL pointer");
+        require_device();
+        uint32_t shift = 0;
+        while ((size_t(1) << shift) < page_tiles) ++shift;
+        check_hip(launch_score_paged_topk(arena_dev, shift, page_table_dev, (uint32_t)max_pages,
+                                          seq_len_dev, score_base_dev, (uint32_t)n_seq,
+                                          (uint32_t)max_len, (uint32_t)n_kv_heads, (uint32_t)group,
+                                          q_coarse_dev, q_sign_dev, scores_dev, (uint32_t)k,
+                                          topk_idx_dev, topk_score_dev,
+                                          static_cast<hipStream_t>(stream)),
+                  "paged score kernel");
+    });
+}
+
+int32_t slha_gpu_ccos_apply(SciRustSlhaTile* tiles_dev, const uint32_t* slots_dev, size_t n,
+                            int32_t op, void* stream) {
+    return ffi_status([&] {
+        if (op != 0 && op != 1) fail(SLHA_ERR_DIMENSION, "unknown CCOS op %d", op);
+        if (n == 0) return;
+        if (!tiles_dev || !slots_dev) fail(SLHA_ERR_NULL, "slha_gpu_ccos_apply received a NULL pointer");
+        require_device();
+        check_hip(launch_ccos_apply(tiles_dev, slots_dev, n, op, static_cast<hipStream_t>(stream)),
+                  "ccos kernel");
+    });
+}
+
+int32_t slha_gpu_synchronize(void* stream) {
+    return ffi_status([&] {
+        require_device();
+        check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+        check_hip(hipGetLastError(), "pending HIP error");
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,1021 @@
+// slha_kernels.hip — gfx950 kernels of the SLHA v2 tile path.
+//
+// Compiled with -ffp-contract=off: every "exact" routine below performs the
+// reference's f32 operations in the reference's order (Rust never contracts
+// a*b+c). Fast routines contract explicitly with fmaf().
+//
+// Kernels:
+//   score_rows_kernel      eq. 2.3 over tile rows, GQA fan-out (tile.rs:267-281)
+//   encode_kernel<CODEC>   key -> tile, mode R/Z (codec/*.rs, scenario.rs:95-114)
+//   prepare_query_kernel   q -> (q_coarse, q_sign) (scenario.rs:70-83)
+//   decode_kernel          tile -> latent (+ sign-sketch residual) (learned.rs:283-321)
+//   validate_kernel        slha-c/src/lib.rs:244-286 on device
+//   ccos_apply_kernel      page_out / drop_correction (ccos.rs:369-397)
+#include "slha_device.h"
+#include "slha_launch.h"
+
+#include <climits>
+
+namespace slha {
+
+// ---------------------------------------------------------------------------
+// Tile loads
+
+__device__ __forceinline__ void load_tile(const uint4* __restrict__ p, uint32_t* w) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint4 v = p[j];
+        w[4 * j + 0] = v.x;
+        w[4 * j + 1] = v.y;
+        w[4 * j + 2] = v.z;
+        w[4 * j + 3] = v.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Scoring.
+//
+// One lane scores one tile against all `group` queries of its row: the tile
+// (128 B) is read from HBM once into 32 VGPRs; queries are wave-uniform, so
+// the compiler reads them through the scalar cache and every MAC is a single
+// v_fma_f32 with an SGPR operand. The tile is decoded one 16-dim group at a
+// time for a chunk of kQC queries, which keeps the register footprint small
+// enough for several waves per SIMD.
+//
+// Fast mode factors the per-group scale out of the group sum:
+//     sum_{d in g} q_d * (a_g * m_d - b_g) = a_g * (sum q_d m_d - b_g/a_g-free offset * Q_g)
+// with m_d a small integer decoded by integer ops (INT4 nibble, TQ3 2*code+corr),
+// Q_g = sum_{d in g} q_d computed once per workgroup into LDS. Mixed/MIX3
+// tiles, whose sections do not align to 16-dim groups, decode to scaled
+// values. EXACT mode evaluates tile.rs:267-281 verbatim (sequential f32, no
+// FMA) and is bit-identical to the scalar reference.
+//
+// A wave whose lanes hold different codecs runs each codec's path with only
+// the matching lanes active; a codec-uniform wave runs exactly one path.
+
+constexpr int kQC = 4;  // queries per chunk
+
+enum : int { kClsInt4 = 0, kClsNF4 = 1, kClsMixed = 2, kClsTQ3 = 3, kClsMix3 = 4 };
+
+__device__ __forceinline__ int codec_class(uint32_t flags) {  // tile.rs:142-157 precedence
+    if (flags & kFlagMixed) return kClsMixed;
+    if (flags & kFlagTQ3) return kClsTQ3;
+    if (flags & kFlagMix3) return kClsMix3;
+    if (flags & kFlagNF4) return kClsNF4;
+    return kClsInt4;
+}
+
+// Fast decode of dims [16g, 16g+16) into m[16]; returns the group factor a
+// and offset b such that the group's dequantised values are a*(m - b).
+template <int CLS>
+__device__ __forceinline__ void decode_group_fast(const uint32_t* w, int g, float s255,
+                                                  const float* cb, float* m, float& a, float& b) {
+    const uint32_t* lw = w;
+    const float gsf = gs_at(w + 30, g);
+    const uint32_t flags = w[29] >> 16;
+    if constexpr (CLS == kClsInt4 || CLS == kClsNF4) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t x = lw[2 * g + k];
+            const uint32_t lo = x & 0x0F0F0F0Fu;
+            const uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t n0 = (lo >> (8 * j)) & 0xFFu, n1 = (hi >> (8 * j)) & 0xFFu;
+                if constexpr (CLS == kClsInt4) {
+                    m[8 * k + 2 * j] = (float)n0;
+                    m[8 * k + 2 * j + 1] = (float)n1;
+                } else {
+                    m[8 * k + 2 * j] = cb[n0];
+                    m[8 * k + 2 * j + 1] = cb[n1];
+                }
+            }
+        }
+        a = gsf * s255;
+        b = CLS == kClsInt4 ? 8.0f : 0.0f;
+    } else if constexpr (CLS == kClsTQ3) {
+        const bool nocorr = (flags & kFlagNoCorr) != 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int d = 16 * g + i;
+            const uint32_t code = bits3_at(lw, 3 * d);
+            const uint32_t corr = nocorr ? 0u : bit_at(lw, 384 + d);
+            m[i] = (float)((code << 1) | corr);
+        }
+        a = 0.5f * gsf * s255;
+        b = nocorr ? 7.0f : 7.5f;
+    } else {  // mixed / MIX3: scaled values, a = 1, b = 0
+        const float s0 = gs_at(w + 30, 0) * s255;
+        const bool nocorr = (flags & kFlagNoCorr) != 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int d = 16 * g + i;
+            if (d < 8) {
+                m[i] = fmaf((float)byte_at(lw, d), s0, -128.0f * s0);
+            } else if (d < 120) {
+                const int ld = d - 8;
+                const float sg = gs_at(w + 30, 1 + ld / 16) * s255;
+                if constexpr (CLS == kClsMixed) {
+                    m[i] = fmaf((float)nib_at(lw, 16 + ld), sg, -8.0f * sg);
+                } else {
+                    const uint32_t code = bits3_at(lw, 64 + 3 * ld);
+                    const uint32_t corr = nocorr ? 0u : bit_at(lw, 400 + ld);
+                    m[i] = fmaf((float)((code << 1) | corr), 0.5f * sg,
+                                (nocorr ? -3.5f : -3.75f) * sg);
+                }
+            } else {
+                m[i] = 0.0f;
+            }
+        }
+        a = 1.0f;
+        b = 0.0f;
+    }
+}
+
+// Exact dequant of dims [16g, 16g+16) (tile.rs:141-246, operation order kept).
+template <int CLS>
+__device__ __forceinline__ void decode_group_exact(const uint32_t* w, int g, const float* cb,
+                                                   float* k) {
+    const uint32_t* lw = w;
+    const uint32_t* gw = w + 30;
+    const float scale = __uint_as_float(w[24]);
+    const bool nocorr = ((w[29] >> 16) & kFlagNoCorr) != 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int d = 16 * g + i;
+        if constexpr (CLS == kClsInt4) {
+            k[i] = (float)((int)nib_at(lw, d) - 8) * group_scale_exact(scale, gs_at(gw, g));
+        } else if constexpr (CLS == kClsNF4) {
+            k[i] = cb[nib_at(lw, d)] * group_scale_exact(scale, gs_at(gw, g));
+        } else if constexpr (CLS == kClsTQ3) {
+            k[i] = tq3_level_exact(lw, 0, 384, d, nocorr) * group_scale_exact(scale, gs_at(gw, g));
+        } else {
+            if (d < 8) {
+                k[i] = (float)((int)byte_at(lw, d) - 128) * section_scale_exact(scale, gs_at(gw, 0));
+            } else if (d < 120) {
+                const int ld = d - 8;
+                const float sec = section_scale_exact(scale, gs_at(gw, 1 + ld / 16));
+                if constexpr (CLS == kClsMixed)
+                    k[i] = (float)((int)nib_at(lw, 16 + ld) - 8) * sec;
+                else
+                    k[i] = tq3_level_exact(lw, 64, 400, ld, nocorr) * sec;
+            } else {
+                k[i] = 0.0f;
+            }
+        }
+    }
+}
+
+// Score one tile (in w) against queries qrow0 .. qrow0+group-1, writing
+// query j's score to out[j * stride + t].
+template <int CLS, bool EXACT, bool HAM>
+__device__ __forceinline__ void score_lane(const uint32_t* w, uint32_t group, size_t qrow0,
+                                           const float* __restrict__ qc,
+                                           const uint32_t* __restrict__ qs, const float* cb,
+                                           const float* qsum, float* __restrict__ out,
+                                           uint32_t* __restrict__ ham, size_t stride,
+                                           uint32_t t) {
+    const float scale = __uint_as_float(w[24]);
+    const float lambda = __uint_as_float(w[25]);
+    const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
+    const float s255 = scale * (1.0f / 255.0f);
+    for (uint32_t j0 = 0; j0 < group; j0 += kQC) {
+        float acc[kQC];
+#pragma unroll
+        for (int c = 0; c < kQC; ++c) acc[c] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            float m[16];
+            if constexpr (EXACT) {
+                decode_group_exact<CLS>(w, g, cb, m);
+#pragma unroll
+                for (int c = 0; c < kQC; ++c) {
+                    if (j0 + c < group) {
+                        const float* q = qc + (qrow0 + j0 + c) * kDC + 16 * g;
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) acc[c] += q[i] * m[i];
+                    }
+                }
+            } else {
+                float a, b;
+                decode_group_fast<CLS>(w, g, s255, cb, m, a, b);
+#pragma unroll
+                for (int c = 0; c < kQC; ++c) {
+                    if (j0 + c < group) {
+                        const float* q = qc + (qrow0 + j0 + c) * kDC + 16 * g;
+                        float p = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) p = fmaf(q[i], m[i], p);
+                        if (CLS != kClsMixed && CLS != kClsMix3)
+                            p = fmaf(-b, qsum[(j0 + c) * 8 + g], p);
+                        acc[c] = fmaf(a, p, acc[c]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < kQC; ++c) {
+            if (j0 + c < group) {
+                const size_t qrow = qrow0 + j0 + c;
+                const uint32_t h = hamming_words(w + 16, qs + qrow * 8);
+                float score = acc[c];
+                if (!warm) {
+                    if constexpr (EXACT)
+                        score = score + lambda * (256.0f - 2.0f * (float)h);
+                    else
+                        score = fmaf(lambda, 256.0f - 2.0f * (float)h, score);
+                }
+                out[(size_t)(j0 + c) * stride + t] = score;
+                if constexpr (HAM) ham[(size_t)(j0 + c) * stride + t] = h;
+            }
+        }
+    }
+}
+
+// NF4 codebook (constants.rs:138-141) staged in LDS.
+__device__ __forceinline__ void stage_codebook(float* cb) {
+    if (threadIdx.x < 16) cb[threadIdx.x] = nf4_level(threadIdx.x);
+}
+
+// Per-(query, group) sums of q for the fast path.
+__device__ __forceinline__ void stage_qsum(const float* __restrict__ qc, size_t qrow0,
+                                           uint32_t group, float* qsum) {
+    for (uint32_t i = threadIdx.x; i < group * 8; i += blockDim.x) {
+        const float* q = qc + (qrow0 + (i >> 3)) * kDC + (i & 7) * 16;
+        float s = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) s += q[d];
+        qsum[i] = s;
+    }
+}
+
+template <bool EXACT, bool HAM>
+__device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group, size_t qrow0,
+                                               const float* __restrict__ qc,
+                                               const uint32_t* __restrict__ qs, const float* cb,
+                                               const float* qsum, float* __restrict__ out,
+                                               uint32_t* __restrict__ ham, size_t stride,
+                                               uint32_t t) {
+    const int cls = codec_class(w[29] >> 16);
+#define SLHA_LANE(C) score_lane<C, EXACT, HAM>(w, group, qrow0, qc, qs, cb, qsum, out, ham, stride, t)
+    if (cls == kClsInt4) SLHA_LANE(kClsInt4);
+    if (cls == kClsNF4) SLHA_LANE(kClsNF4);
+    if (cls == kClsTQ3) SLHA_LANE(kClsTQ3);
+    if (cls == kClsMixed) SLHA_LANE(kClsMixed);
+    if (cls == kClsMix3) SLHA_LANE(kClsMix3);
+#undef SLHA_LANE
+}
+
+template <bool EXACT, bool HAM>
+__global__ __launch_bounds__(256) void score_rows_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs,
+    float* __restrict__ scores, uint32_t* __restrict__ ham) {
+    __shared__ float qsum[kMaxGroup * 8];
+    __shared__ float cb[16];
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    stage_codebook(cb);
+    if constexpr (!EXACT) stage_qsum(qc, qrow0, group, qsum);
+    __syncthreads();
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_tok) return;
+    uint32_t w[32];
+    load_tile(tiles + ((size_t)row * n_tok + t) * 8, w);
+    score_dispatch<EXACT, HAM>(w, group, qrow0, qc, qs, cb, qsum, scores + qrow0 * n_tok,
+                               HAM ? ham + qrow0 * n_tok : nullptr, n_tok, t);
+}
+
+// CCOS paged scoring: block (x, y) covers tokens [256x, 256x+256) of
+// (sequence s, KV head h) with y = s*n_kv + h; token t lives in physical page
+// page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
+__global__ __launch_bounds__(256) void score_paged_kernel(
+    const uint4* __restrict__ arena, uint32_t page_shift, const uint32_t* __restrict__ page_table,
+    uint32_t max_pages, const uint32_t* __restrict__ seq_len,
+    const unsigned long long* __restrict__ score_base, uint32_t n_kv, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float qsum[kMaxGroup * 8];
+    __shared__ float cb[16];
+    const uint32_t y = blockIdx.y;
+    const uint32_t s = y / n_kv, h = y - s * n_kv;
+    const uint32_t len = seq_len[s];
+    if (blockIdx.x * blockDim.x >= len) return;  // whole block past this sequence
+    const size_t qrow0 = (size_t)y * group;
+    stage_codebook(cb);
+    stage_qsum(qc, qrow0, group, qsum);
+    __syncthreads();
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= len) return;
+    const uint32_t phys = page_table[(size_t)y * max_pages + (t >> page_shift)];
+    const size_t slot = ((size_t)phys << page_shift) + (t & ((1u << page_shift) - 1u));
+    uint32_t w[32];
+    load_tile(arena + slot * 8, w);
+    float* out = scores + score_base[s] + (size_t)h * group * len;
+    score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, qsum, out, nullptr, len, t);
+}
+
+// ---------------------------------------------------------------------------
+// Top-k per score row: score descending, ties to the lower token index.
+//
+// One 1024-thread workgroup per (sequence, query head) row. Scores map to
+// order-preserving u32 keys; a three-pass radix select (11 + 11 + 10 bits,
+// histograms in LDS) finds the k-th largest key T and how many keys equal to
+// T are needed; a final pass in token order collects every key > T plus the
+// lowest-index keys == T; the k winners are bitonic-sorted in LDS.
+
+constexpr int kTopkThreads = 1024;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    // -0.0 and +0.0 compare equal, so they share a key (ties then go by index).
+    const uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Finds the digit bin holding the need-th largest element (1-based) from the
+// top of hist[nbins]; returns the bin and the count strictly above it.
+__device__ __forceinline__ void select_bin(uint32_t* hist, int nbins, uint32_t need,
+                                          uint32_t* sh_bin, uint32_t* sh_above) {
+    // Suffix sums: hist[i] <- sum_{j >= i} hist[j] (Hillis-Steele over LDS).
+    for (int off = 1; off < nbins; off <<= 1) {
+        uint32_t v[2] = {0, 0};
+        for (int r = 0; r < 2; ++r) {
+            const int i = threadIdx.x + r * kTopkThreads;
+            if (i < nbins) v[r] = hist[i] + ((i + off < nbins) ? hist[i + off] : 0u);
+        }
+        __syncthreads();
+        for (int r = 0; r < 2; ++r) {
+            const int i = threadIdx.x + r * kTopkThreads;
+            if (i < nbins) hist[i] = v[r];
+        }
+        __syncthreads();
+    }
+    for (int r = 0; r < 2; ++r) {
+        const int i = threadIdx.x + r * kTopkThreads;
+        if (i < nbins) {
+            const uint32_t ge = hist[i];
+            const uint32_t gt = (i + 1 < nbins) ? hist[i + 1] : 0u;
+            if (ge >= need && gt < need) {
+                *sh_bin = (uint32_t)i;
+                *sh_above = gt;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
+    const float* __restrict__ scores, const uint32_t* __restrict__ seq_len,
+    const unsigned long long* __restrict__ score_base, uint32_t hq, uint32_t k,
+    uint32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
+    __shared__ uint32_t hist[2048];
+    __shared__ uint32_t sel_key[kMaxTopK];
+    __shared__ uint32_t sel_idx[kMaxTopK];
+    __shared__ uint32_t sh_bin, sh_above, sh_count, sh_eq_taken;
+    __shared__ uint32_t wave_eq[kTopkThreads / 64];
+    const uint32_t row = blockIdx.x;
+    const uint32_t s = row / hq, qh = row - s * hq;
+    const uint32_t len = seq_len[s];
+    const float* sc = scores + score_base[s] + (size_t)qh * len;
+    const uint32_t kk = k < len ? k : len;
+
+    uint32_t prefix = 0, prefix_mask = 0, need = kk;
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    for (int pass = 0; pass < 3 && kk > 0; ++pass) {
+        const int nb = 1 << widths[pass];
+        for (int i = threadIdx.x; i < 2048; i += kTopkThreads) hist[i] = 0u;
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < len; i += kTopkThreads) {
+            const uint32_t key = order_key(sc[i]);
+            if ((key & prefix_mask) == prefix)
+                atomicAdd(&hist[(key >> shifts[pass]) & (uint32_t)(nb - 1)], 1u);
+        }
+        __syncthreads();
+        select_bin(hist, nb, need, &sh_bin, &sh_above);
+        need -= sh_above;
+        prefix |= sh_bin << shifts[pass];
+        prefix_mask |= (uint32_t)(nb - 1) << shifts[pass];
+    }
+    const uint32_t thr = prefix;  // exact k-th largest key; `need` keys == thr are taken
+
+    if (threadIdx.x == 0) {
+        sh_count = 0;
+        sh_eq_taken = 0;
+    }
+    __syncthreads();
+    // Collect in token order: chunks of kTopkThreads, ranks of == thr by
+    // ballot prefix so the lowest indices win the ties.
+    for (uint32_t base = 0; base < len && kk > 0; base += kTopkThreads) {
+        const uint32_t i = base + threadIdx.x;
+        uint32_t key = 0;
+        bool gt = false, eq = false;
+        if (i < len) {
+            key = order_key(sc[i]);
+            gt = key > thr;
+            eq = key == thr;
+        }
+        if (gt) {
+            const uint32_t slot = atomicAdd(&sh_count, 1u);
+            if (slot < kMaxTopK) {
+                sel_key[slot] = key;
+                sel_idx[slot] = i;
+            }
+        }
+        const unsigned long long bal = __ballot(eq);
+        const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        if (lane == 0) wave_eq[wv] = (uint32_t)__popcll(bal);
+        __syncthreads();
+        uint32_t before = 0;
+        for (uint32_t j = 0; j < wv; ++j) before += wave_eq[j];
+        const uint32_t rank = sh_eq_taken + before +
+                              (uint32_t)__popcll(bal & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+        if (eq && rank < need) {
+            const uint32_t slot = atomicAdd(&sh_count, 1u);
+            if (slot < kMaxTopK) {
+                sel_key[slot] = key;
+                sel_idx[slot] = i;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t tot = 0;
+            for (uint32_t j = 0; j < kTopkThreads / 64; ++j) tot += wave_eq[j];
+            sh_eq_taken += tot;
+        }
+        __syncthreads();
+    }
+    // Pad to kMaxTopK and bitonic-sort by (key desc, idx asc).
+    for (uint32_t i = threadIdx.x; i < kMaxTopK; i += kTopkThreads) {
+        if (i >= kk) {
+            sel_key[i] = 0u;
+            sel_idx[i] = 0xFFFFFFFFu;
+        }
+    }
+    __syncthreads();
+    for (uint32_t size = 2; size <= kMaxTopK; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = threadIdx.x; i < kMaxTopK; i += kTopkThreads) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    // "a before b" iff a.key > b.key or (equal and a.idx < b.idx)
+                    const uint32_t ka = sel_key[i], kb = sel_key[j];
+                    const uint32_t ia = sel_idx[i], ib = sel_idx[j];
+                    const bool a_first = ka > kb || (ka == kb && ia < ib);
+                    const bool up = (i & size) == 0;
+                    if (up != a_first) {
+                        sel_key[i] = kb;
+                        sel_key[j] = ka;
+                        sel_idx[i] = ib;
+                        sel_idx[j] = ia;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < k; i += kTopkThreads) {
+        const size_t o = (size_t)row * k + i;
+        if (i < kk) {
+            topk_idx[o] = sel_idx[i];
+            topk_val[o] = key_to_float(sel_key[i]);
+        } else {
+            topk_idx[o] = 0xFFFFFFFFu;
+            topk_val[o] = -INFINITY;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Encode: Rust numeric semantics.
+
+__device__ __forceinline__ int32_t rs_i32(float f) {  // `f as i32`
+    if (isnan(f)) return 0;
+    if (f >= 2147483648.0f) return INT_MAX;
+    if (f <= -2147483648.0f) return INT_MIN;
+    return (int32_t)f;
+}
+__device__ __forceinline__ uint32_t rs_u8(float f) {  // `f as u8`
+    if (isnan(f)) return 0u;
+    if (f >= 255.0f) return 255u;
+    if (f <= 0.0f) return 0u;
+    return (uint32_t)f;
+}
+__device__ __forceinline__ float rs_clampf(float x, float lo, float hi) {  // f32::clamp
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+__device__ __forceinline__ int32_t clampi(int32_t x, int32_t lo, int32_t hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
+template <int LO, int HI>
+__device__ __forceinline__ float absmax(const float* v) {
+    float m = 0.0f;
+#pragma unroll
+    for (int d = LO; d < HI; ++d) m = fmaxf(m, fabsf(v[d]));
+    return m;
+}
+
+// (global, gs) from the per-section steps: int4.rs:43-50 and its twins.
+__device__ __forceinline__ float group_bytes(const float* steps, uint32_t* gsw) {
+    float global = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) global = fmaxf(global, steps[g]);
+    if (!(global > 0.0f)) global = 1.0f;
+    gsw[0] = gsw[1] = 0u;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const float r = roundf(steps[g] / global * 255.0f);
+        gsw[g >> 2] |= rs_u8(rs_clampf(r, 1.0f, 255.0f)) << (8 * (g & 3));
+    }
+    return global;
+}
+
+__device__ __forceinline__ void put_bits(uint32_t* lw, int p, uint32_t v) {
+    const int wi = p >> 5, sh = p & 31;
+    lw[wi] |= v << sh;
+    if (sh > 29 && wi + 1 < 16) lw[wi + 1] |= v >> (32 - sh);
+}
+
+__device__ __forceinline__ uint32_t nf4_nearest(float t) {  // nf4.rs:7-18
+    uint32_t best = 0;
+    float best_d = INFINITY;
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+        const float dd = fabsf(t - nf4_level(i));
+        if (dd < best_d) {
+            best_d = dd;
+            best = i;
+        }
+    }
+    return best;
+}
+
+// One TQ3 code + correction bit (tq3.rs:31-46, mix3.rs:44-58).
+__device__ __forceinline__ void tq3_put(uint32_t* lw, int codes_bit0, int corr_bit0, int ld,
+                                        float val, float eff) {
+    const float t = val / eff;
+    const uint32_t code = (uint32_t)clampi(rs_i32(roundf(t + 3.5f)), 0, 7);
+    put_bits(lw, codes_bit0 + 3 * ld, code);
+    const float level = (float)code - 3.5f;
+    if (t - level > 0.0f) put_bits(lw, corr_bit0 + ld, 1u);
+}
+
+// Quantise v into (lw, scale, gsw); returns the codec flag.
+template <int CODEC>
+__device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float* scale_out,
+                                             uint32_t* gsw) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lw[i] = 0u;
+    float steps[8];
+    if constexpr (CODEC == kCodecInt4Single) {  // int4.rs:9-24
+        const float max_abs = absmax<0, 128>(v);
+        const float scale = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
+#pragma unroll
+        for (int d = 0; d < 128; ++d) {
+            const int32_t q = rs_i32(roundf(v[d] / scale));
+            put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+        }
+        gsw[0] = gsw[1] = 0xFFFFFFFFu;
+        *scale_out = scale;
+        return 0u;
+    } else if constexpr (CODEC == kCodecInt4Grouped || CODEC == kCodecNF4 ||
+                         CODEC == kCodecTQ3) {  // int4.rs:34-63, nf4.rs:23-57, tq3.rs:10-49
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            float m = 0.0f;
+#pragma unroll
+            for (int d = 16 * g; d < 16 * g + 16; ++d) m = fmaxf(m, fabsf(v[d]));
+            steps[g] = CODEC == kCodecInt4Grouped ? m / 7.0f
+                       : CODEC == kCodecNF4       ? m
+                                                  : m / 3.5f;
+        }
+        const float global = group_bytes(steps, gsw);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const float eff = global * (gs_at(gsw, g) / 255.0f);
+#pragma unroll
+            for (int d = 16 * g; d < 16 * g + 16; ++d) {
+                if constexpr (CODEC == kCodecInt4Grouped) {
+                    const int32_t q = rs_i32(roundf(v[d] / eff));
+                    put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+                } else if constexpr (CODEC == kCodecNF4) {
+                    const float t = eff > 0.0f ? rs_clampf(v[d] / eff, -1.0f, 1.0f) : 0.0f;
+                    put_bits(lw, 4 * d, nf4_nearest(t));
+                } else {
+                    tq3_put(lw, 0, 384, d, v[d], eff);
+                }
+            }
+        }
+        *scale_out = global;
+        return CODEC == kCodecInt4Grouped ? 0u : (CODEC == kCodecNF4 ? kFlagNF4 : kFlagTQ3);
+    } else {  // mixed.rs:13-57, mix3.rs:11-62
+        steps[0] = absmax<0, 8>(v) / 127.0f;
+#pragma unroll
+        for (int g = 0; g < 7; ++g) {
+            float m = 0.0f;
+#pragma unroll
+            for (int d = 8 + 16 * g; d < 24 + 16 * g; ++d) m = fmaxf(m, fabsf(v[d]));
+            steps[1 + g] = CODEC == kCodecMixed ? m / 7.0f : m / 3.5f;
+        }
+        const float global = group_bytes(steps, gsw);
+        const float eff_hi = global * (gs_at(gsw, 0) / 255.0f);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int32_t q = rs_i32(roundf(v[d] / eff_hi));
+            put_bits(lw, 8 * d, (uint32_t)(clampi(q, -128, 127) + 128));
+        }
+#pragma unroll
+        for (int g = 0; g < 7; ++g) {
+            const float eff = global * (gs_at(gsw, 1 + g) / 255.0f);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int ld = 16 * g + i;
+                if constexpr (CODEC == kCodecMixed) {
+                    const int32_t q = rs_i32(roundf(v[8 + ld] / eff));
+                    put_bits(lw, 64 + 4 * ld, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+                } else {
+                    tq3_put(lw, 64, 400, ld, v[8 + ld], eff);
+                }
+            }
+        }
+        *scale_out = global;
+        return CODEC == kCodecMixed ? kFlagMixed : kFlagMix3;
+    }
+}
+
+// Exact dequant of dim d for a statically known codec (tile.rs:141-246).
+template <int CODEC>
+__device__ __forceinline__ float dequant_dim(const uint32_t* lw, const uint32_t* gsw, float scale,
+                                             int d) {
+    if constexpr (CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped) {
+        return (float)((int)nib_at(lw, d) - 8) * group_scale_exact(scale, gs_at(gsw, d / 16));
+    } else if constexpr (CODEC == kCodecNF4) {
+        return nf4_level(nib_at(lw, d)) * group_scale_exact(scale, gs_at(gsw, d / 16));
+    } else if constexpr (CODEC == kCodecTQ3) {
+        return tq3_level_exact(lw, 0, 384, d, false) * group_scale_exact(scale, gs_at(gsw, d / 16));
+    } else {
+        if (d < 8) return (float)((int)byte_at(lw, d) - 128) * section_scale_exact(scale, gs_at(gsw, 0));
+        if (d >= 120) return 0.0f;
+        const int ld = d - 8;
+        const float sec = section_scale_exact(scale, gs_at(gsw, 1 + ld / 16));
+        if constexpr (CODEC == kCodecMixed)
+            return (float)((int)nib_at(lw, 16 + ld) - 8) * sec;
+        else
+            return tq3_level_exact(lw, 64, 400, ld, false) * sec;
+    }
+}
+
+// Orthonormal FWHT of 128 register values (incoherence.rs:45-70), after the
+// +-1 diagonal (incoherence.rs:114-125). Butterflies of one stage are
+// independent, so evaluating them in register order is bit-identical.
+__device__ __forceinline__ void rht128(float* v, const float* __restrict__ diag, float inv) {
+#pragma unroll
+    for (int i = 0; i < 128; ++i) v[i] *= diag[i];
+#pragma unroll
+    for (int h = 1; h < 128; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 128; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; ++j) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 128; ++i) v[i] *= inv;
+}
+
+// Packed sign(Z v) (scenario.rs:70-83): bit s = (sum_k Z[s][k] * v[k] < 0),
+// sequential f32 from 0.0 with no contraction. Z rows are wave-uniform and are
+// read through the scalar cache.
+__device__ __forceinline__ void sign_bits_exact(const float* v, const float* __restrict__ z,
+                                                uint32_t* bits) {
+    // Four rows at a time: four independent sequential accumulation chains
+    // give the VALU instruction-level parallelism without changing any
+    // row's own operation order.
+#pragma unroll
+    for (int wd = 0; wd < 8; ++wd) {
+        uint32_t word = 0u;
+        for (int b = 0; b < 32; b += 4) {
+            const float* zr = z + (size_t)(32 * wd + b) * kDC;
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kDC; ++k) {
+                const float x = v[k];
+                a0 += zr[k] * x;
+                a1 += zr[kDC + k] * x;
+                a2 += zr[2 * kDC + k] * x;
+                a3 += zr[3 * kDC + k] * x;
+            }
+            word |= ((a0 < 0.0f ? 1u : 0u) | (a1 < 0.0f ? 2u : 0u) | (a2 < 0.0f ? 4u : 0u) |
+                     (a3 < 0.0f ? 8u : 0u))
+                    << b;
+        }
+        bits[wd] = word;
+    }
+}
+
+__device__ __forceinline__ void load_vec128(const void* __restrict__ src, int dtype, size_t idx,
+                                            float* v) {
+    if (dtype == kDtypeBF16) {
+        const uint4* p = reinterpret_cast<const uint4*>(src) + idx * 16;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint4 x = p[j];
+            const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[8 * j + 2 * k] = __uint_as_float(u[k] << 16);
+                v[8 * j + 2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+            }
+        }
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(src) + idx * 32;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const float4 x = p[j];
+            v[4 * j] = x.x;
+            v[4 * j + 1] = x.y;
+            v[4 * j + 2] = x.z;
+            v[4 * j + 3] = x.w;
+        }
+    }
+}
+
+// Tile encode, mode R (e = key - dequant) or mode Z (e = 0). One lane per key.
+template <int CODEC>
+__global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ keys, int dtype,
+                                                     uint64_t n_keys, uint32_t n_tok,
+                                                     uint32_t n_kv, uint32_t pos0,
+                                                     int residual_mode, int warm,
+                                                     const float* __restrict__ z,
+                                                     const float* __restrict__ diag,
+                                                     float lambda_c, float rht_inv,
+                                                     uint4* __restrict__ tiles) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_keys) return;
+    const uint32_t row = (uint32_t)(i / n_tok);
+    const uint32_t t = (uint32_t)(i - (uint64_t)row * n_tok);
+
+    float v[kDC];
+    load_vec128(keys, dtype, i, v);
+
+    uint32_t lw[16], gsw[2];
+    float scale;
+    const uint32_t codec_flag = quantize<CODEC>(v, lw, &scale, gsw);
+
+    uint32_t bits[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float sigma = 0.0f, lambda = 0.0f;
+    if (residual_mode == kResidualR) {
+        bool finite = true;
+        double acc = 0.0;
+#pragma unroll
+        for (int d = 0; d < kDC; ++d) {
+            v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, scale, d);
+            finite = finite && isfinite(v[d]);
+            const double x = (double)v[d];
+            acc = fma(x, x, acc);  // x*x is exact in f64, so this equals acc + x*x
+        }
+        sigma = finite ? (float)sqrt(acc / 128.0) : __uint_as_float(0x7FC00000u);  // metrics.rs:207-226
+        lambda = sigma * lambda_c;
+        if (diag) rht128(v, diag, rht_inv);
+        sign_bits_exact(v, z, bits);
+    }
+
+    const uint32_t flags = codec_flag | (warm ? kFlagWarm : 0u);
+    const uint32_t pos = pos0 + t;
+    uint4* out = tiles + i * 8;
+    out[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    out[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    out[2] = make_uint4(lw[8], lw[9], lw[10], lw[11]);
+    out[3] = make_uint4(lw[12], lw[13], lw[14], lw[15]);
+    out[4] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
+    out[5] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
+    out[6] = make_uint4(__float_as_uint(scale), __float_as_uint(lambda), __float_as_uint(sigma), pos);
+    out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
+}
+
+// Query preparation: q_coarse = q, q_sign = sign(Z * RHT(q)).
+__global__ __launch_bounds__(256) void prepare_query_kernel(const void* __restrict__ q, int dtype,
+                                                            uint64_t n_q,
+                                                            const float* __restrict__ z,
+                                                            const float* __restrict__ diag,
+                                                            float rht_inv, float* __restrict__ qc,
+                                                            uint4* __restrict__ qs) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_q) return;
+    float v[kDC];
+    load_vec128(q, dtype, i, v);
+    float4* qo = reinterpret_cast<float4*>(qc) + i * 32;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) qo[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    if (diag) rht128(v, diag, rht_inv);
+    uint32_t bits[8];
+    sign_bits_exact(v, z, bits);
+    qs[2 * i] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
+    qs[2 * i + 1] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
+}
+
+// Decode: dequant_latent (tile.rs:249-255); optionally add the sign-sketch
+// residual estimate of reconstruct_from_tile (learned.rs:283-321, identity
+// latent, no RHT): key[i] += (+-1 * scale_r) * Z[s][i] in s order.
+__global__ __launch_bounds__(256) void decode_kernel(const uint4* __restrict__ tiles, uint64_t n,
+                                                     const float* __restrict__ z,
+                                                     float sqrt_half_pi, float* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t w[32];
+    load_tile(tiles + i * 8, w);
+    const uint32_t flags = w[29] >> 16;
+    float k[kDC];
+    dequant_exact(w, w + 30, __uint_as_float(w[24]), flags, k);
+    if (z) {
+        const float sc = __uint_as_float(w[26]) * sqrt_half_pi / 256.0f;
+        for (int s = 0; s < kDS; ++s) {
+            const float sgn = ((w[16 + (s >> 5)] >> (s & 31)) & 1u) ? -1.0f : 1.0f;
+            const float f = sgn * sc;
+            const float* zr = z + (size_t)s * kDC;
+#pragma unroll
+            for (int d = 0; d < kDC; ++d) k[d] += f * zr[d];
+        }
+    }
+    float4* o = reinterpret_cast<float4*>(out) + i * 32;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[j] = make_float4(k[4 * j], k[4 * j + 1], k[4 * j + 2], k[4 * j + 3]);
+}
+
+// Validation (slha-c/src/lib.rs:244-286). Records the lowest failing index.
+__global__ __launch_bounds__(256) void validate_kernel(const uint4* __restrict__ tiles, uint64_t n,
+                                                       unsigned long long* __restrict__ status) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint4 m0 = tiles[i * 8 + 6];
+    const uint4 m1 = tiles[i * 8 + 7];
+    const uint32_t flags = m1.y >> 16;
+    const float sc = __uint_as_float(m0.x), la = __uint_as_float(m0.y), si = __uint_as_float(m0.z);
+    int code = 0;
+    if (flags & ~kKnownFlags)
+        code = -6;
+    else if (__popc(flags & kCodecFlags) > 1)
+        code = -6;
+    else if ((flags & kFlagNoCorr) && !(flags & (kFlagTQ3 | kFlagMix3)))
+        code = -6;
+    else if (!isfinite(sc) || !isfinite(la) || !isfinite(si))
+        code = -5;
+    else if (sc < 0.0f || la < 0.0f || si < 0.0f)
+        code = -6;
+    if (code != 0) {
+        const unsigned long long key = ((unsigned long long)(i + 1) << 8) | (unsigned long long)(-code);
+        atomicMin(status, key);
+    }
+}
+
+// CCOS ladder (ccos.rs:369-397) on device tiles.
+__global__ __launch_bounds__(256) void ccos_apply_kernel(uint4* __restrict__ tiles,
+                                                         const uint32_t* __restrict__ slots,
+                                                         uint64_t n, int op) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint4* t = tiles + (size_t)slots[i] * 8;
+    uint4 m0 = t[6], m1 = t[7];
+    uint32_t flags = m1.y >> 16;
+    if (op == 0) {  // page_out: residual := 0, lambda := 0, |WARM
+        t[4] = make_uint4(0, 0, 0, 0);
+        t[5] = make_uint4(0, 0, 0, 0);
+        m0.y = 0u;
+        flags |= kFlagWarm;
+        t[6] = m0;
+    } else {  // drop_correction
+        const int nb = (flags & kFlagTQ3) ? 16 : ((flags & kFlagMix3) ? 14 : 0);
+        if (nb == 0 || (flags & kFlagNoCorr)) return;
+        uint4 l3 = t[3];  // latent bytes 48..63
+        if (nb == 16) {
+            l3 = make_uint4(0, 0, 0, 0);
+        } else {  // bytes 50..63: keep bytes 48, 49
+            l3.x &= 0x0000FFFFu;
+            l3.y = l3.z = l3.w = 0u;
+        }
+        t[3] = l3;
+        flags |= kFlagNoCorr;
+    }
+    m1.y = (m1.y & 0xFFFFu) | (flags << 16);
+    t[7] = m1;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+
+hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
+                             const float* qc, const uint64_t* qs, bool exact, float* scores,
+                             uint32_t* ham, hipStream_t s) {
+    if (n_rows == 0 || n_tok == 0 || group == 0) return hipSuccess;
+    dim3 grid((n_tok + 255) / 256, n_rows);
+    const uint4* tp = static_cast<const uint4*>(tiles);
+    const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
+    if (exact) {
+        if (ham)
+            score_rows_kernel<true, true><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+        else
+            score_rows_kernel<true, false><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+    } else {
+        if (ham)
+            score_rows_kernel<false, true><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+        else
+            score_rows_kernel<false, false><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
+                                  const uint32_t* page_table, uint32_t max_pages,
+                                  const uint32_t* seq_len, const uint64_t* score_base,
+                                  uint32_t n_seq, uint32_t max_len, uint32_t n_kv, uint32_t group,
+                                  const float* qc, const uint64_t* qs, float* scores, uint32_t k,
+                                  uint32_t* topk_idx, float* topk_val, hipStream_t s) {
+    if (n_seq == 0 || max_len == 0) return hipSuccess;
+    const auto* base = reinterpret_cast<const unsigned long long*>(score_base);
+    dim3 grid((max_len + 255) / 256, n_seq * n_kv);
+    score_paged_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(arena), page_shift,
+                                            page_table, max_pages, seq_len, base, n_kv, group, qc,
+                                            reinterpret_cast<const uint32_t*>(qs), scores);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || k == 0) return e;
+    topk_rows_kernel<<<n_seq * n_kv * group, kTopkThreads, 0, s>>>(scores, seq_len, base,
+                                                                    n_kv * group, k, topk_idx,
+                                                                    topk_val);
+    return hipGetLastError();
+}
+
+hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
+                         uint32_t n_kv, uint32_t pos0, int codec, int residual_mode, int warm,
+                         const float* z, const float* diag, float lambda_c, float rht_inv,
+                         void* tiles, hipStream_t s) {
+    if (n_keys == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n_keys + 255) / 256));
+    uint4* tp = static_cast<uint4*>(tiles);
+#define SLHA_ENC(C)                                                                         \
+    encode_kernel<C><<<grid, 256, 0, s>>>(keys, dtype, n_keys, n_tok, n_kv, pos0, residual_mode, \
+                                          warm, z, diag, lambda_c, rht_inv, tp)
+    switch (codec) {
+        case kCodecInt4Single: SLHA_ENC(kCodecInt4Single); break;
+        case kCodecInt4Grouped: SLHA_ENC(kCodecInt4Grouped); break;
+        case kCodecNF4: SLHA_ENC(kCodecNF4); break;
+        case kCodecMixed: SLHA_ENC(kCodecMixed); break;
+        case kCodecTQ3: SLHA_ENC(kCodecTQ3); break;
+        case kCodecMix3: SLHA_ENC(kCodecMix3); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef SLHA_ENC
+    return hipGetLastError();
+}
+
+hipError_t launch_prepare_queries(const void* q, int dtype, uint64_t n_q, const float* z,
+                                  const float* diag, float rht_inv, float* qc, uint64_t* qs,
+                                  hipStream_t s) {
+    if (n_q == 0) return hipSuccess;
+    prepare_query_kernel<<<(unsigned)((n_q + 255) / 256), 256, 0, s>>>(
+        q, dtype, n_q, z, diag, rht_inv, qc, reinterpret_cast<uint4*>(qs));
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, float sqrt_half_pi,
+                         float* out, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    decode_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<const uint4*>(tiles), n,
+                                                             z_or_null, sqrt_half_pi, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    validate_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        static_cast<const uint4*>(tiles), n, reinterpret_cast<unsigned long long*>(status));
+    return hipGetLastError();
+}
+
+__global__ void fill_u64_kernel(uint64_t* p, uint64_t n, uint64_t value) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = value;
+}
+
+hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    fill_u64_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    ccos_apply_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<uint4*>(tiles), slots,
+                                                                 n, op);
+    return hipGetLastError();
+}
+
+}  // namespace slha

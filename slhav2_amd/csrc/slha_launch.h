@@ -1,0 +1,42 @@
+// slha_launch.h — host-side launchers of the gfx950 kernels (internal; the
+// public surface is include/slha.h and include/slha_gpu.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace slha {
+
+// Codec ids (slha.h:32-37).
+constexpr int kCodecInt4Single = 0, kCodecInt4Grouped = 1, kCodecNF4 = 2, kCodecMixed = 3,
+              kCodecTQ3 = 4, kCodecMix3 = 5;
+constexpr int kDtypeF32 = 0, kDtypeBF16 = 1;
+constexpr int kResidualZ = 0, kResidualR = 1;
+// Largest query group one scoring launch serves (LDS holds group*8 sums).
+constexpr uint32_t kMaxGroup = 256;
+// Largest k of the paged top-k (a power of two: the winners are bitonic-sorted).
+constexpr uint32_t kMaxTopK = 256;
+
+hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
+                             const float* qc, const uint64_t* qs, bool exact, float* scores,
+                             uint32_t* ham, hipStream_t s);
+hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
+                                  const uint32_t* page_table, uint32_t max_pages,
+                                  const uint32_t* seq_len, const uint64_t* score_base,
+                                  uint32_t n_seq, uint32_t max_len, uint32_t n_kv, uint32_t group,
+                                  const float* qc, const uint64_t* qs, float* scores, uint32_t k,
+                                  uint32_t* topk_idx, float* topk_val, hipStream_t s);
+hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
+                         uint32_t n_kv, uint32_t pos0, int codec, int residual_mode, int warm,
+                         const float* z, const float* diag, float lambda_c, float rht_inv,
+                         void* tiles, hipStream_t s);
+hipError_t launch_prepare_queries(const void* q, int dtype, uint64_t n_q, const float* z,
+                                  const float* diag, float rht_inv, float* qc, uint64_t* qs,
+                                  hipStream_t s);
+hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, float sqrt_half_pi,
+                         float* out, hipStream_t s);
+hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s);
+hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s);
+hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s);
+
+}  // namespace slha

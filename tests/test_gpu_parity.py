@@ -1,0 +1,335 @@
+"""GPU parity: every HIP entry point against the CPU oracle on identical inputs.
+
+Bars (from the reference's own tests and BASELINE.json):
+  * tile bytes (codes, residual bits, sigma, lambda, metadata): bit-exact;
+  * Hamming distances: bit-exact;
+  * SCORE_EXACT scores: bit-identical to tile.rs's scalar path;
+  * SCORE_FAST scores: |gpu - ref| <= 1e-3 * (1 + |ref|)
+    (scirust/src/attention/slha_v2/tests.rs:923, scirust/tests/properties.rs:73);
+  * top-k indices: exact, ties to the lower token index.
+"""
+import json
+
+import numpy as np
+import pytest
+
+import oracle_ffi as o
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+FLAG_SETS = [0, 1, 2, 3, 4, 5, 8, 9, 8 | 16, 8 | 16 | 1, 32, 33, 32 | 16]
+
+
+@pytest.fixture(scope="module")
+def s(torch_cuda):
+    import slhav2_amd
+
+    return slhav2_amd
+
+
+@pytest.fixture(scope="module")
+def torch(torch_cuda):
+    return torch_cuda
+
+
+def dev(torch, a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def tiles_np(t):
+    return t.cpu().numpy().reshape(-1, 128).copy().view(o.TILE_DTYPE).reshape(-1)
+
+
+def random_tiles(n, seed, flag_sets=FLAG_SETS):
+    r = np.random.default_rng(seed)
+    t = np.zeros(n, o.TILE_DTYPE)
+    t["latent_kv"] = r.integers(0, 256, (n, 64), dtype=np.uint8)
+    t["residual_bitmap"] = r.integers(0, 2**63, (n, 4), dtype=np.uint64) * 2 + r.integers(0, 2, (n, 4), dtype=np.uint64)
+    t["scale"] = (r.random(n) * 2 + 0.01).astype(np.float32)
+    t["dynamic_lambda"] = np.abs(r.normal(size=n) * 0.1).astype(np.float32)
+    t["residual_sigma"] = r.random(n).astype(np.float32)
+    t["group_scales"] = r.integers(1, 256, (n, 8), dtype=np.uint8)
+    t["flags"] = np.asarray(flag_sets, np.uint16)[r.integers(0, len(flag_sets), n)]
+    t["position"] = np.arange(n, dtype=np.uint32)
+    return t
+
+
+def keys_for(seed, n, kind="gauss"):
+    r = o.Rng(seed)
+    k = r.gaussian(n * 128).reshape(n, 128)
+    if kind == "scaled":  # C4: per-token scale log-uniform in [0.1, 10]
+        u = np.array([r.next_unit() for _ in range(n)], np.float32)
+        k = (k * (np.float32(0.1) * np.float32(100.0) ** u)[:, None]).astype(np.float32)
+    if kind == "student":  # C3: Student-t(4) with 4 outlier channels x20
+        z = r.gaussian(n * 4 * 128).reshape(n, 128, 4)
+        k = (k / np.sqrt((z ** 2).mean(-1))).astype(np.float32)
+        k[:, [3, 17, 64, 100]] *= np.float32(20.0)
+    k[0] = 0.0
+    k[1] = ((np.arange(128) - 64) / 16.0).astype(np.float32)
+    return k.astype(np.float32)
+
+
+def assert_tol(got, ref):
+    bad = np.abs(got.astype(np.float64) - ref) > TOL * (1 + np.abs(ref.astype(np.float64)))
+    assert not bad.any(), (np.argwhere(bad)[:5], got[bad][:5], ref[bad][:5])
+
+
+def test_audit_known_answer(s):
+    rep = json.loads(s.audit())
+    assert rep["ok"] is True and rep["kat_basic_usage"] == -8.0 and rep["tile_size"] == 128
+    assert "gfx950" in rep["arch"]
+
+
+@pytest.mark.parametrize("codec", range(6))
+@pytest.mark.parametrize("rht", [False, True])
+@pytest.mark.parametrize("kind", ["gauss", "scaled", "student"])
+def test_encode_bit_exact(s, torch, codec, rht, kind):
+    n_rows, n_tok, n_kv = 2, 193, 2
+    keys = keys_for(1000 + codec, n_rows * n_tok, kind)
+    with s.Model(seed=31 + codec, rht=rht) as m:
+        z, diag = m.projection()
+        for dtype in (torch.float32, torch.bfloat16):
+            kin = keys if dtype == torch.float32 else o.bf16_round(keys)
+            kd = dev(torch, kin.reshape(n_rows, n_tok, 128), dtype)
+            tiles = tiles_np(s.gpu_encode(m, kd, codec, n_kv_heads=n_kv, pos0=5))
+            for r in range(n_rows):
+                ref = o.encode(kin[r * n_tok:(r + 1) * n_tok], codec, 1, z, diag if rht else None,
+                               pos0=5, head=r % n_kv)
+                got = tiles[r * n_tok:(r + 1) * n_tok]
+                assert got.tobytes() == ref.tobytes(), (codec, rht, kind, dtype, r)
+
+
+@pytest.mark.parametrize("codec", [0, 2, 4])
+def test_encode_mode_z_and_warm(s, torch, codec):
+    keys = keys_for(7, 300)
+    with s.Model(seed=5, rht=False, residual_mode=s.RESIDUAL_Z) as m:
+        z, _ = m.projection()
+        t = tiles_np(s.gpu_encode(m, dev(torch, keys), codec, warm=True))
+    ref = o.encode(keys, codec, 0, z)
+    ref["flags"] |= 1
+    assert t.tobytes() == ref.tobytes()
+
+
+@pytest.mark.parametrize("rht", [False, True])
+def test_prepare_queries_bit_exact(s, torch, rht):
+    q = keys_for(11, 97, "scaled")
+    with s.Model(seed=12, rht=rht) as m:
+        z, diag = m.projection()
+        for dtype in (torch.float32, torch.bfloat16):
+            qin = q if dtype == torch.float32 else o.bf16_round(q)
+            qc, qs = s.gpu_prepare_queries(m, dev(torch, qin, dtype))
+            qs = qs.cpu().numpy().view(np.uint64)
+            assert np.array_equal(qc.cpu().numpy(), qin)
+            for i in range(len(q)):
+                assert np.array_equal(qs[i], o.query_sign(qin[i], z, diag if rht else None))
+
+
+@pytest.mark.parametrize("group", [1, 4, 5, 8])
+def test_score_exact_bit_identical_and_hamming(s, torch, group):
+    n_rows, n_tok = 3, 777
+    tiles = random_tiles(n_rows * n_tok, 40 + group)
+    r = np.random.default_rng(group)
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
+    td = dev(torch, tiles.view(np.uint8).reshape(n_rows, n_tok, 128))
+    qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
+    exact, ham = s.gpu_score(td, qd, qsd, group=group, mode=s.SCORE_EXACT, hamming=True)
+    fast = s.gpu_score(td, qd, qsd, group=group, mode=s.SCORE_FAST)
+    exact, ham, fast = exact.cpu().numpy(), ham.cpu().numpy(), fast.cpu().numpy()
+    for row in range(n_rows):
+        for j in range(group):
+            qi = row * group + j
+            ref, href = o.score(tiles[row * n_tok:(row + 1) * n_tok], q[qi], qs[qi])
+            assert np.array_equal(exact[qi].view(np.uint32), ref.view(np.uint32))
+            assert np.array_equal(ham[qi].astype(np.uint32), href)
+            assert_tol(fast[qi], ref)
+
+
+def test_score_fast_wide_group_c4_shape(s, torch):
+    # C4 shape: one row, 64 queries per tile (TQ3 + RHT tiles).
+    keys = keys_for(99, 2048, "scaled")
+    with s.Model(seed=4, rht=True) as m:
+        tiles = s.gpu_encode(m, dev(torch, o.bf16_round(keys)), s.CODEC_TQ3)
+        q = o.bf16_round(keys_for(98, 64))
+        qc, qs = s.gpu_prepare_queries(m, dev(torch, q, torch.bfloat16))
+        sc = s.gpu_score(tiles, qc, qs, group=64).cpu().numpy()
+    tnp = tiles_np(tiles)
+    qsn = qs.cpu().numpy().view(np.uint64)
+    for j in range(0, 64, 7):
+        ref, _ = o.score(tnp, q[j], qsn[j])
+        assert_tol(sc[j], ref)
+
+
+def test_host_abi_paths(s, torch):
+    with s.Model(seed=21, rht=False) as m:
+        z, _ = m.projection()
+        keys = keys_for(5, 40)
+        for codec in range(6):
+            t = s.encode_key(m, keys[3], position=9, codec=codec)
+            ref = o.encode(keys[3:4], codec, 1, z, pos0=9)[0]
+            assert t.tobytes() == ref.tobytes()
+            assert np.array_equal(s.decode_latent(m, t), o.dequant(ref))
+        qc, qs = s.prepare_query(m, keys[7])
+        assert np.array_equal(qc, keys[7]) and np.array_equal(qs, o.query_sign(keys[7], z))
+        tiles = o.encode(keys, 1, 1, z)
+        got = s.score_tiles(m, tiles, qc, qs)
+        ref, _ = o.score(tiles, qc, qs)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        assert s.score_tile(m, tiles[4], qc, qs) == ref[4]
+        assert s.process_tile(tiles[4], qc, qs) == ref[4]
+        # decode_key: latent + sign-sketch estimate (learned.rs:283-321)
+        dk = s.decode_key(m, tiles[2])
+        sc = np.float32(tiles[2]["residual_sigma"]) * np.float32(np.sqrt(np.float32(np.pi / 2))) / np.float32(256)
+        bits = np.unpackbits(tiles[2]["residual_bitmap"].view(np.uint8), bitorder="little")
+        est = o.dequant(tiles[2]).astype(np.float64) + ((1 - 2 * bits.astype(np.float64)) * sc) @ z
+        assert np.max(np.abs(dk - est)) < 1e-4
+        # a bad tile anywhere leaves every output untouched (slha.h:193-195)
+        bad = tiles.copy()
+        bad[5]["flags"] = 0x40
+        out = np.full(len(bad), 3.0, np.float32)
+        rc = s.lib.slha_score_tiles(m.handle, bad.ctypes.data, len(bad), qc.ctypes.data,
+                                    qs.ctypes.data, out.ctypes.data)
+        assert rc == s.ERR_INVALID_TILE and np.all(out == 3.0)
+
+
+def test_validate_kernel(s, torch):
+    tiles = random_tiles(5000, 3)
+    tiles[4000]["flags"] = 2 | 8
+    tiles[1234]["scale"] = np.nan
+    tiles[3000]["dynamic_lambda"] = -1.0
+    res = s.gpu_validate_tiles(dev(torch, tiles.view(np.uint8).reshape(-1, 128)))
+    first = next(i for i in range(len(tiles)) if o.validate(tiles[i]) != 0)
+    assert res == (first, o.validate(tiles[first])) == (1234, -5)
+    assert s.gpu_validate_tiles(dev(torch, random_tiles(100, 4).view(np.uint8).reshape(-1, 128))) is None
+
+
+def test_ccos_apply(s, torch):
+    tiles = random_tiles(512, 8, [0, 2, 8, 32, 8 | 16])
+    td = dev(torch, tiles.view(np.uint8).reshape(-1, 128))
+    slots = np.arange(0, 512, 3, dtype=np.int32)
+    s.gpu_ccos_apply(td, dev(torch, slots), 1)
+    s.gpu_ccos_apply(td, dev(torch, slots[::2].copy()), 0)
+    want = tiles.copy()
+    for i in slots:
+        want[i:i + 1] = o.drop_correction(want[i])[0]
+    for i in slots[::2]:
+        want[i:i + 1] = o.page_out(want[i])
+    assert tiles_np(td).tobytes() == want.tobytes()
+
+
+def build_paged(lens, n_kv, page_tiles, seed, tiles_src):
+    """Cut per-(seq, head) token streams into pages and shuffle them in one arena."""
+    r = np.random.default_rng(seed)
+    max_pages = max(1, max(-(-l // page_tiles) for l in lens))
+    logical = []
+    for si, l in enumerate(lens):
+        for h in range(n_kv):
+            for p in range(-(-l // page_tiles)):
+                logical.append((si, h, p))
+    perm = r.permutation(len(logical))
+    arena = np.zeros(max(len(logical), 1) * page_tiles, o.TILE_DTYPE)
+    table = np.zeros((len(lens), n_kv, max_pages), np.int32)
+    for phys, li in enumerate(perm):
+        si, h, p = logical[li]
+        table[si, h, p] = phys
+        src = tiles_src[(si, h)]
+        chunk = src[p * page_tiles:(p + 1) * page_tiles]
+        arena[phys * page_tiles:phys * page_tiles + len(chunk)] = chunk
+    return arena, table, max_pages
+
+
+@pytest.mark.parametrize("const_scores", [False, True])
+def test_paged_topk(s, torch, const_scores):
+    lens = [1, 63, 64, 1000, 5000, 300]
+    n_kv, group, page_tiles, k = 2, 4, 256, 64
+    r = np.random.default_rng(11)
+    src = {}
+    for si, l in enumerate(lens):
+        for h in range(n_kv):
+            t = random_tiles(l, 100 * si + h, [0, 2])
+            warm = r.random(l) < 0.3
+            for i in np.nonzero(warm)[0]:
+                t[i:i + 1] = o.page_out(t[i])
+            if const_scores:  # identical tiles: every score ties, top-k = first k tokens
+                t[:] = t[0]
+            src[(si, h)] = t
+    arena, table, max_pages = build_paged(lens, n_kv, page_tiles, 5, src)
+    hq = n_kv * group
+    q = r.normal(size=(len(lens) * hq, 128)).astype(np.float32)
+    qs = r.integers(0, 2**63, (len(lens) * hq, 4), dtype=np.uint64)
+    scores, idx, val = s.gpu_score_paged_topk(
+        dev(torch, arena.view(np.uint8).reshape(-1, 128)), page_tiles, dev(torch, table),
+        max_pages, dev(torch, np.asarray(lens, np.int32)), n_kv, group, dev(torch, q),
+        dev(torch, qs.view(np.int64)), k)
+    scores, idx, val = scores.cpu().numpy(), idx.cpu().numpy().view(np.uint32), val.cpu().numpy()
+    base = 0
+    for si, l in enumerate(lens):
+        for qh in range(hq):
+            h = qh // group
+            got = scores[base + qh * l: base + (qh + 1) * l]
+            ref, _ = o.score(src[(si, h)], q[si * hq + qh], qs[si * hq + qh])
+            assert_tol(got, ref)
+            ti, tv = o.topk(got, k)
+            assert np.array_equal(idx[si, qh], ti), (si, qh)
+            if const_scores:
+                assert list(ti[: min(k, l)]) == list(range(min(k, l)))
+            assert np.array_equal(val[si, qh][: min(k, l)], tv[: min(k, l)])
+        base += hq * l
+
+
+def test_c1_cpu_reference_config(s, torch):
+    # 4096 f32 N(0,1) keys, INT4, one f32 N(0,1) query.
+    keys = o.Rng(0x5EED0000).gaussian(4096 * 128).reshape(4096, 128)
+    q = o.Rng(0x5EED0001).gaussian(128)
+    with s.Model(seed=0x5EED0002) as m:
+        z, _ = m.projection()
+        td = s.gpu_encode(m, dev(torch, keys), s.CODEC_INT4_SINGLE)
+        qc, qs = s.gpu_prepare_queries(m, dev(torch, q[None]))
+        exact, ham = s.gpu_score(td, qc, qs, mode=s.SCORE_EXACT, hamming=True)
+        fast = s.gpu_score(td, qc, qs)
+    ref_t = o.encode(keys, 0, 1, z)
+    assert tiles_np(td).tobytes() == ref_t.tobytes()
+    ref, href = o.score(ref_t, q, o.query_sign(q, z))
+    assert np.array_equal(exact.cpu().numpy()[0].view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(ham.cpu().numpy()[0].astype(np.uint32), href)
+    assert_tol(fast.cpu().numpy()[0], ref)
+
+
+def test_c2_full_size_properties(s, torch):
+    # BASELINE configs[1] at full size: 8 KV heads x 32768 bf16 keys, 32 queries.
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+    keys = torch.randn((8, 32768, 128), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((32, 128), device="cuda", generator=g).to(torch.bfloat16)
+    with s.Model(seed=0x5EED0002) as m:
+        z, _ = m.projection()
+        tiles = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE, n_kv_heads=8)
+        qc, qs = s.gpu_prepare_queries(m, q)
+        fast = s.gpu_score(tiles, qc, qs, group=4)
+        exact, ham = s.gpu_score(tiles, qc, qs, group=4, mode=s.SCORE_EXACT, hamming=True)
+    fast, exact, ham = fast.cpu().numpy(), exact.cpu().numpy(), ham.cpu().numpy()
+    assert fast.shape == (32, 32768)
+    assert_tol(fast, exact)
+    # sampled oracle checks: tile bytes, Hamming, exact scores
+    kn = keys.float().cpu().numpy()
+    tn = tiles.cpu().numpy().reshape(8, 32768, 128)
+    qn, qsn = q.float().cpu().numpy(), qs.cpu().numpy().view(np.uint64)
+    r = np.random.default_rng(0)
+    for h in range(8):
+        idx = np.sort(r.choice(32768, 256, replace=False))
+        ref_t = o.encode(kn[h, idx], 0, 1, z)
+        ref_t["position"] = idx
+        ref_t["token_id"] = idx
+        ref_t["head_id"] = h
+        got_t = tn[h, idx].copy().view(o.TILE_DTYPE).reshape(-1)
+        assert got_t.tobytes() == ref_t.tobytes()
+        for j in range(4):
+            qi = 4 * h + j
+            ref, href = o.score(ref_t, qn[qi], qsn[qi])
+            assert np.array_equal(exact[qi, idx].view(np.uint32), ref.view(np.uint32))
+            assert np.array_equal(ham[qi, idx].astype(np.uint32), href)
+    # Hamming is an integer in [0, 256] with mean ~128 for independent signs
+    assert ham.min() >= 0 and ham.max() <= 256 and abs(ham.mean() - 128) < 2
