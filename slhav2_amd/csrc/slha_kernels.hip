@@ -15,6 +15,7 @@
 #include "slha_launch.h"
 
 #include <climits>
+#include <cstdlib>
 
 namespace slha {
 
@@ -53,7 +54,6 @@ __device__ __forceinline__ void load_tile(const uint4* __restrict__ p, uint32_t*
 // A wave whose lanes hold different codecs runs each codec's path with only
 // the matching lanes active; a codec-uniform wave runs exactly one path.
 
-constexpr int kQC = 4;  // queries per chunk
 
 enum : int { kClsInt4 = 0, kClsNF4 = 1, kClsMixed = 2, kClsTQ3 = 3, kClsMix3 = 4 };
 
@@ -167,69 +167,379 @@ __device__ __forceinline__ void decode_group_exact(const uint32_t* w, int g, con
 }
 
 // Score one tile (in w) against queries qrow0 .. qrow0+group-1, writing
-// query j's score to out[j * stride + t].
+// query j's score to out[j * stride + t]. This per-lane path serves EXACT
+// mode and waves whose lanes hold different codecs. It decodes one 16-dim
+// group at a time for one query at a time; the empty asm makes the tile words
+// opaque per query so the compiler cannot hoist all 128 decoded values out of
+// the query loop (which would cost 128 VGPRs and most of the occupancy).
 template <int CLS, bool EXACT, bool HAM>
-__device__ __forceinline__ void score_lane(const uint32_t* w, uint32_t group, size_t qrow0,
+__device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group, size_t qrow0,
                                            const float* __restrict__ qc,
                                            const uint32_t* __restrict__ qs, const float* cb,
-                                           const float* qsum, float* __restrict__ out,
-                                           uint32_t* __restrict__ ham, size_t stride,
-                                           uint32_t t) {
-    const float scale = __uint_as_float(w[24]);
-    const float lambda = __uint_as_float(w[25]);
-    const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
-    const float s255 = scale * (1.0f / 255.0f);
-    for (uint32_t j0 = 0; j0 < group; j0 += kQC) {
-        float acc[kQC];
+                                           float* __restrict__ out, uint32_t* __restrict__ ham,
+                                           size_t stride, uint32_t t) {
+#pragma unroll 1
+    for (uint32_t j = 0; j < group; ++j) {
+        uint32_t w[32];
 #pragma unroll
-        for (int c = 0; c < kQC; ++c) acc[c] = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            w[i] = w_in[i];
+            asm volatile("" : "+v"(w[i]));
+        }
+        const float scale = __uint_as_float(w[24]);
+        const float lambda = __uint_as_float(w[25]);
+        const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
+        const float s255 = scale * (1.0f / 255.0f);
+        const size_t qrow = qrow0 + j;
+        const float* qrowp = qc + qrow * kDC;
+        float acc = 0.0f;
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
             float m[16];
+            const float* q = qrowp + 16 * g;
             if constexpr (EXACT) {
                 decode_group_exact<CLS>(w, g, cb, m);
 #pragma unroll
-                for (int c = 0; c < kQC; ++c) {
-                    if (j0 + c < group) {
-                        const float* q = qc + (qrow0 + j0 + c) * kDC + 16 * g;
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) acc[c] += q[i] * m[i];
-                    }
-                }
+                for (int i = 0; i < 16; ++i) acc += q[i] * m[i];
             } else {
                 float a, b;
                 decode_group_fast<CLS>(w, g, s255, cb, m, a, b);
+                float p = 0.0f;
 #pragma unroll
-                for (int c = 0; c < kQC; ++c) {
-                    if (j0 + c < group) {
-                        const float* q = qc + (qrow0 + j0 + c) * kDC + 16 * g;
-                        float p = 0.0f;
+                for (int i = 0; i < 16; ++i) p = fmaf(q[i], m[i] - b, p);
+                acc = fmaf(a, p, acc);
+            }
+        }
+        const uint32_t h = hamming_words(w + 16, qs + qrow * 8);
+        float score = acc;
+        if (!warm) {
+            if constexpr (EXACT)
+                score = score + lambda * (256.0f - 2.0f * (float)h);
+            else
+                score = fmaf(lambda, 256.0f - 2.0f * (float)h, score);
+        }
+        out[(size_t)j * stride + t] = score;
+        if constexpr (HAM) ham[(size_t)j * stride + t] = h;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fast path on the matrix cores (v_mfma_f32_4x4x1_16b_f32).
+//
+// One wave scores its 64 tiles against a chunk of 4 queries. In the 16-block
+// 4x4x1 layout lane l supplies B column l and receives C column l in its four
+// result registers, while row r of block l/4 takes A from lane 4*(l/4) + r.
+// So lane l feeds dim d of ITS tile as B and q_{l%4}[d] as A, and after 128
+// MFMAs (one per dim) holds the four query dot products of its own tile: no
+// cross-lane traffic. B is the dequantised value a_g*(m - b_g) of
+// decode_group_fast (one FMA per dim); products and sums are f32.
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kQStride = 132;      // LDS row stride of a staged query (floats)
+constexpr uint32_t kQStrideH = 264;     // u16 words per staged f16 query (512 B + 16 B pad)
+constexpr uint32_t kMfmaMaxGroup = 64;  // queries staged in LDS per workgroup
+
+// Dynamic LDS of the fast kernels: f32 staged queries (MFMA f32 paths), f16
+// hi/lo staged queries and their 2^e factors (INT4 f16 path).
+struct StagedQueries {
+    float* q32;
+    uint16_t* q16;
+    float* qexp;
+};
+
+// rows_alloc: staged query rows the launch allocated (staging_bytes(rows_alloc)).
+__device__ __forceinline__ StagedQueries carve_staging(float* smem, uint32_t rows_alloc) {
+    const uint32_t rows = rows_alloc;
+    StagedQueries sq;
+    sq.q32 = smem;
+    sq.q16 = reinterpret_cast<uint16_t*>(smem + rows * kQStride);
+    sq.qexp = reinterpret_cast<float*>(sq.q16 + rows * kQStrideH);
+    return sq;
+}
+
+__host__ __device__ constexpr uint32_t staging_rows(uint32_t group) { return (group + 3u) & ~3u; }
+__host__ __device__ constexpr size_t staging_bytes(uint32_t rows_alloc) {
+    return (size_t)rows_alloc * (kQStride * 4u + kQStrideH * 2u + 4u);
+}
+
+template <int CLS>
+__device__ __forceinline__ void score_wave_mfma(const uint32_t* w_in, bool valid, uint32_t group,
+                                                size_t qrow0, const float* qlds, const float* cb,
+                                                const uint32_t* __restrict__ qs,
+                                                float* __restrict__ out, size_t stride,
+                                                uint32_t t) {
+    const uint32_t r = threadIdx.x & 3u;
+#pragma unroll 1
+    for (uint32_t c0 = 0; c0 < group; c0 += 4) {
+        // Opaque per chunk: keeps the decode inside the loop (see score_lane).
+        uint32_t w[32];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) p = fmaf(q[i], m[i], p);
-                        if (CLS != kClsMixed && CLS != kClsMix3)
-                            p = fmaf(-b, qsum[(j0 + c) * 8 + g], p);
-                        acc[c] = fmaf(a, p, acc[c]);
-                    }
+        for (int i = 0; i < 32; ++i) {
+            w[i] = w_in[i];
+            asm volatile("" : "+v"(w[i]));
+        }
+        const float lambda = __uint_as_float(w[25]);
+        const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
+        const float s255 = __uint_as_float(w[24]) * (1.0f / 255.0f);
+        const float* qa = qlds + (c0 + r) * kQStride;
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            float m[16], ga, gb;
+            decode_group_fast<CLS>(w, g, s255, cb, m, ga, gb);
+            const float off = -ga * gb;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(qa + 16 * g + i);
+                const float qv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    // dequantised value a_g * (m - b_g), then one MFMA step
+                    const float v = (CLS == kClsMixed || CLS == kClsMix3) ? m[i + k]
+                                                                          : fmaf(m[i + k], ga, off);
+                    acc = __builtin_amdgcn_mfma_f32_4x4x1f32(qv[k], v, acc, 0, 0, 0);
                 }
             }
         }
 #pragma unroll
-        for (int c = 0; c < kQC; ++c) {
-            if (j0 + c < group) {
-                const size_t qrow = qrow0 + j0 + c;
-                const uint32_t h = hamming_words(w + 16, qs + qrow * 8);
-                float score = acc[c];
-                if (!warm) {
-                    if constexpr (EXACT)
-                        score = score + lambda * (256.0f - 2.0f * (float)h);
-                    else
-                        score = fmaf(lambda, 256.0f - 2.0f * (float)h, score);
-                }
-                out[(size_t)(j0 + c) * stride + t] = score;
-                if constexpr (HAM) ham[(size_t)(j0 + c) * stride + t] = h;
+        for (int rr = 0; rr < 4; ++rr) {
+            if (c0 + rr < group) {
+                float sc = acc[rr];
+                const uint32_t h = hamming_words(w + 16, qs + (qrow0 + c0 + rr) * 8);
+                if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
+                if (valid) out[(size_t)(c0 + rr) * stride + t] = sc;
             }
         }
     }
+}
+
+// INT4 fast path on v_mfma_f32_4x4x4_16b_f16 (same lane = tile layout,
+// four dims per MFMA). B is the exact integer (n - 8) * gs in f16
+// (|.| <= 2040 < 2^11), built from magic-number halves: for a latent dword x
+// holding nibbles n0..n7, (x & 0x000F000F) | 0x64006400 is the f16 pair
+// (1024 + n0, 1024 + n4) and (x & 0x00F000F0) | 0x64006400 is
+// (1024 + 16 n1, 1024 + 16 n5); one packed add / fma recovers n - 8 exactly
+// and one packed mul applies gs. The dims of a dword therefore enter the
+// MFMA in the order (d0, d4, d1, d5 | d2, d6, d3, d7), and the staged
+// queries use the same order. Each query is prescaled by an exact power of
+// two 2^-e (|q 2^-e| <= 1) and split into f16 hi + lo halves, so q is carried
+// to ~2^-22 relative and every product is exact in the f32 accumulator. The
+// tile's scale/255 and 2^e are applied once per (tile, query) at the end.
+
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+
+__device__ __forceinline__ v2h as_v2h(uint32_t u) { return __builtin_bit_cast(v2h, u); }
+
+__device__ __forceinline__ void score_wave_int4_f16(const uint32_t* w_in, bool valid,
+                                                    uint32_t group, size_t qrow0,
+                                                    const uint16_t* qh, const float* qexp,
+                                                    const uint32_t* __restrict__ qs,
+                                                    float* __restrict__ out, size_t stride,
+                                                    uint32_t t) {
+    const uint32_t r = threadIdx.x & 3u;
+    const v2h k_lo = v2h{(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const v2h k_sixteenth = v2h{(_Float16)0.0625f, (_Float16)0.0625f};
+    const v2h k_hi = v2h{(_Float16)-72.0f, (_Float16)-72.0f};
+#pragma unroll 1
+    for (uint32_t c0 = 0; c0 < group; c0 += 4) {
+        uint32_t w[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            w[i] = w_in[i];
+            asm volatile("" : "+v"(w[i]));
+        }
+        const uint16_t* qa = qh + (c0 + r) * kQStrideH;
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            const float gsf = gs_at(w + 30, p >> 1);
+            const v2h gs2 = v2h{(_Float16)gsf, (_Float16)gsf};
+            const uint32_t x = w[p];
+            const uint32_t x8 = x >> 8;
+            const v2h l0 = (as_v2h((x & 0x000F000Fu) | 0x64006400u) + k_lo) * gs2;
+            const v2h l1 = __builtin_elementwise_fma(as_v2h((x & 0x00F000F0u) | 0x64006400u),
+                                                     k_sixteenth, k_hi) * gs2;
+            const v2h l2 = (as_v2h((x8 & 0x000F000Fu) | 0x64006400u) + k_lo) * gs2;
+            const v2h l3 = __builtin_elementwise_fma(as_v2h((x8 & 0x00F000F0u) | 0x64006400u),
+                                                     k_sixteenth, k_hi) * gs2;
+            const v4h b01 = v4h{l0.x, l0.y, l1.x, l1.y};
+            const v4h b23 = v4h{l2.x, l2.y, l3.x, l3.y};
+            const uint4 hq = *reinterpret_cast<const uint4*>(qa + 16 * p);      // hi halves
+            const uint4 lq = *reinterpret_cast<const uint4*>(qa + 16 * p + 8);  // lo halves
+            const v4h a_hi01 = __builtin_bit_cast(v4h, make_uint2(hq.x, hq.y));
+            const v4h a_hi23 = __builtin_bit_cast(v4h, make_uint2(hq.z, hq.w));
+            const v4h a_lo01 = __builtin_bit_cast(v4h, make_uint2(lq.x, lq.y));
+            const v4h a_lo23 = __builtin_bit_cast(v4h, make_uint2(lq.z, lq.w));
+            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi01, b01, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo01, b01, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi23, b23, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo23, b23, acc, 0, 0, 0);
+        }
+        const float s255 = __uint_as_float(w[24]) * (1.0f / 255.0f);
+        const float lambda = __uint_as_float(w[25]);
+        const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            if (c0 + rr < group) {
+                float sc = acc[rr] * (s255 * qexp[c0 + rr]);
+                const uint32_t h = hamming_words(w + 16, qs + (qrow0 + c0 + rr) * 8);
+                if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
+                if (valid) out[(size_t)(c0 + rr) * stride + t] = sc;
+            }
+        }
+    }
+}
+
+// Stage queries for the f16 INT4 path: per query, dword position p (8 dims)
+// holds 8 hi halves then 8 lo halves in the (d0, d4, d1, d5, d2, d6, d3, d7)
+// order; qexp[j] = 2^e with |q_j| <= 2^e. One wave per query; rows past
+// `group` up to a multiple of 4 are zero.
+// Runs the MFMA path when every valid lane of the wave holds the same codec
+// (always true for arrays written by one encoder call); returns false when
+// the wave must fall back to the per-lane path.
+__device__ __forceinline__ bool score_wave_try_mfma(const uint32_t* w, bool valid, uint32_t group,
+                                                    size_t qrow0, const float* qlds, const float* cb,
+                                                    const uint16_t* qh, const float* qexp,
+                                                    const uint32_t* __restrict__ qs,
+                                                    float* __restrict__ out, size_t stride,
+                                                    uint32_t t) {
+    const int cls = valid ? codec_class(w[29] >> 16) : -1;
+    const int c0 = __builtin_amdgcn_readfirstlane(cls);
+    if (c0 < 0 || !__all(cls == c0 || cls < 0)) return false;
+    if (c0 == kClsInt4 && qh) {
+        score_wave_int4_f16(w, valid, group, qrow0, qh, qexp, qs, out, stride, t);
+        return true;
+    }
+#define SLHA_WAVE(C) score_wave_mfma<C>(w, valid, group, qrow0, qlds, cb, qs, out, stride, t)
+    switch (c0) {
+        case kClsInt4: SLHA_WAVE(kClsInt4); break;
+        case kClsNF4: SLHA_WAVE(kClsNF4); break;
+        case kClsTQ3: SLHA_WAVE(kClsTQ3); break;
+        case kClsMixed: SLHA_WAVE(kClsMixed); break;
+        default: SLHA_WAVE(kClsMix3); break;
+    }
+#undef SLHA_WAVE
+    return true;
+}
+
+// Queries of one row staged in LDS for the MFMA A operand.
+// Rows group..round_up(group, 4) are zero so the MFMA A operand needs no mask.
+__device__ __forceinline__ uint32_t staged_rows(uint32_t group) { return (group + 3u) & ~3u; }
+
+__device__ __forceinline__ void stage_queries(const float* __restrict__ qc, size_t qrow0,
+                                              uint32_t group, float* qlds) {
+    const uint32_t n = staged_rows(group) * 32u;  // float4s
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t q = i >> 5, d4 = i & 31u;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (q < group) v = reinterpret_cast<const float4*>(qc + (qrow0 + q) * kDC)[d4];
+        *reinterpret_cast<float4*>(qlds + q * kQStride + 4 * d4) = v;
+    }
+}
+
+// Two-phase query staging for group <= kRegStageMaxGroup: stage_issue() only
+// issues the global loads into registers, so the kernel can issue its tile
+// loads right after them; stage_commit() then waits for the (older) query
+// loads alone and fills both LDS copies. Together with lds_barrier(), which
+// waits for LDS traffic only, the tile loads stay in flight across the
+// workgroup barrier.
+constexpr uint32_t kRegStageMaxGroup = 16;
+
+// ROWS = staged query rows (4 or 16); the launch allocates staging_bytes(ROWS).
+template <uint32_t ROWS>
+struct QueryRegs {
+    float4 a[ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1];  // f32 copy, float4 (threadIdx.x + 256 k) mod 32*ROWS
+    float2 b[ROWS / 4];                                  // f16 copy: row wave + 4 k
+};
+
+template <uint32_t ROWS>
+__device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t qrow0,
+                                            uint32_t group, QueryRegs<ROWS>& r) {
+    // Branch-free (clamped rows, zeroed in stage_commit) for exact wait counts.
+    constexpr uint32_t NA = ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1;
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (uint32_t k = 0; k < NA; ++k) {
+        const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u), q = i >> 5;
+        const uint32_t qq = q < group ? q : group - 1u;
+        r.a[k] = reinterpret_cast<const float4*>(qc + (qrow0 + qq) * kDC)[i & 31u];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < ROWS / 4; ++k) {
+        const uint32_t j = wv + 4u * k;
+        const uint32_t jj = j < group ? j : group - 1u;
+        r.b[k] = reinterpret_cast<const float2*>(qc + (qrow0 + jj) * kDC)[lane];
+    }
+}
+
+__device__ __forceinline__ void stage_f16_row(float v0, float v1, uint32_t j, uint16_t* qh,
+                                              float* qexp) {
+    const uint32_t lane = threadIdx.x & 63u;
+    float m = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    int e = 0;  // smallest power of two >= m (m = 0 -> 1)
+    if (m > 0.0f) {
+        (void)frexpf(m, &e);
+        if (ldexpf(1.0f, e - 1) == m) e -= 1;
+    }
+    const float inv = ldexpf(1.0f, -e);
+    const float d[2] = {v0 * inv, v1 * inv};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t dim = 2 * lane + k;
+        const _Float16 hi = (_Float16)d[k];
+        const _Float16 lo = (_Float16)(d[k] - (float)hi);
+        // position of dim inside its dword's (d0, d4, d1, d5, d2, d6, d3, d7) order
+        const uint32_t n = dim & 7u, pword = dim >> 3;
+        const uint32_t slot = (n & 1u ? 2u : 0u) + (n >> 2) + (n & 2u ? 4u : 0u);
+        qh[j * kQStrideH + 16 * pword + slot] = __builtin_bit_cast(uint16_t, hi);
+        qh[j * kQStrideH + 16 * pword + 8 + slot] = __builtin_bit_cast(uint16_t, lo);
+    }
+    if (lane == 0) qexp[j] = ldexpf(1.0f, e);
+}
+
+__device__ __forceinline__ void stage_queries_f16(const float* __restrict__ qc, size_t qrow0,
+                                                  uint32_t group, uint16_t* qh, float* qexp) {
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t rows = (group + 3u) & ~3u;
+    for (uint32_t j = wv; j < rows; j += nw) {
+        float2 v = make_float2(0.0f, 0.0f);
+        if (j < group) v = reinterpret_cast<const float2*>(qc + (qrow0 + j) * kDC)[lane];
+        stage_f16_row(v.x, v.y, j, qh, qexp);
+    }
+}
+
+// Writes all ROWS staged rows (rows past `group` are zero; threads past
+// 32*ROWS float4s rewrite identical values), so no branch disturbs the
+// vector-memory wait counts.
+template <uint32_t ROWS>
+__device__ __forceinline__ void stage_commit(const QueryRegs<ROWS>& r, uint32_t group,
+                                             const StagedQueries& sq) {
+    constexpr uint32_t NA = ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1;
+    const uint32_t wv = threadIdx.x >> 6;
+#pragma unroll
+    for (uint32_t k = 0; k < NA; ++k) {
+        const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u), q = i >> 5;
+        const float m = q < group ? 1.0f : 0.0f;  // value select: no pointer select
+        const float4 x = r.a[k];
+        *reinterpret_cast<float4*>(sq.q32 + q * kQStride + 4 * (i & 31u)) =
+            make_float4(x.x * m, x.y * m, x.z * m, x.w * m);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < ROWS / 4; ++k) {
+        const uint32_t j = wv + 4u * k;
+        const float m = j < group ? 1.0f : 0.0f;
+        const float2 x = r.b[k];
+        stage_f16_row(x.x * m, x.y * m, j, sq.q16, sq.qexp);
+    }
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // NF4 codebook (constants.rs:138-141) staged in LDS.
@@ -237,27 +547,14 @@ __device__ __forceinline__ void stage_codebook(float* cb) {
     if (threadIdx.x < 16) cb[threadIdx.x] = nf4_level(threadIdx.x);
 }
 
-// Per-(query, group) sums of q for the fast path.
-__device__ __forceinline__ void stage_qsum(const float* __restrict__ qc, size_t qrow0,
-                                           uint32_t group, float* qsum) {
-    for (uint32_t i = threadIdx.x; i < group * 8; i += blockDim.x) {
-        const float* q = qc + (qrow0 + (i >> 3)) * kDC + (i & 7) * 16;
-        float s = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 16; ++d) s += q[d];
-        qsum[i] = s;
-    }
-}
-
 template <bool EXACT, bool HAM>
 __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group, size_t qrow0,
                                                const float* __restrict__ qc,
                                                const uint32_t* __restrict__ qs, const float* cb,
-                                               const float* qsum, float* __restrict__ out,
-                                               uint32_t* __restrict__ ham, size_t stride,
-                                               uint32_t t) {
+                                               float* __restrict__ out, uint32_t* __restrict__ ham,
+                                               size_t stride, uint32_t t) {
     const int cls = codec_class(w[29] >> 16);
-#define SLHA_LANE(C) score_lane<C, EXACT, HAM>(w, group, qrow0, qc, qs, cb, qsum, out, ham, stride, t)
+#define SLHA_LANE(C) score_lane<C, EXACT, HAM>(w, group, qrow0, qc, qs, cb, out, ham, stride, t)
     if (cls == kClsInt4) SLHA_LANE(kClsInt4);
     if (cls == kClsNF4) SLHA_LANE(kClsNF4);
     if (cls == kClsTQ3) SLHA_LANE(kClsTQ3);
@@ -266,24 +563,174 @@ __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group
 #undef SLHA_LANE
 }
 
+// Coalesced tile fetch for a wave's 64 consecutive tiles (8 KiB): load j of
+// lane l reads the 16 B at byte 1024 j + 16 l, so every load instruction of the
+// wave covers 1 KiB of contiguous HBM, and writes it to a wave-private LDS
+// region; lane l then reads back tile l. Chunk c of tile u sits at uint4
+// slot 8u + (c ^ (u & 7)): the XOR swizzle keeps both the writes and the
+// lane-per-tile reads free of bank conflicts. Tiles at or past n_valid read
+// as zero. Only lanes of one wave touch the region, so no barrier is needed.
+__device__ __forceinline__ void fetch_tiles_issue(const uint4* __restrict__ base, uint32_t n_valid,
+                                                  uint4* v) {
+    // Branch-free: out-of-range lanes re-read uint4 0 of the wave's first
+    // tile (always valid: the caller passes n_valid >= 1) and are zeroed when
+    // the data arrives, so the wait counters stay exact.
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t idx = 64u * j + lane;  // uint4 index within the 8 KiB
+        v[j] = base[(idx >> 3) < n_valid ? idx : 0u];
+    }
+}
+
+__device__ __forceinline__ void fetch_tiles_mask(uint32_t n_valid, uint4* v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (((64u * j + lane) >> 3) >= n_valid) v[j] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+__device__ __forceinline__ void fetch_tiles_transpose(const uint4* v, uint4* region, uint32_t* w) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t idx = 64u * j + lane;
+        const uint32_t u = idx >> 3, c = idx & 7u;
+        region[8u * u + (c ^ (u & 7u))] = v[j];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS writes done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint4 x = region[8u * lane + (c ^ (lane & 7u))];
+        w[4 * c + 0] = x.x;
+        w[4 * c + 1] = x.y;
+        w[4 * c + 2] = x.z;
+        w[4 * c + 3] = x.w;
+    }
+}
+
+// Per-lane scoring of tile rows: EXACT mode, Hamming output, or groups too
+// large for the staged MFMA path.
 template <bool EXACT, bool HAM>
 __global__ __launch_bounds__(256) void score_rows_kernel(
     const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
     const float* __restrict__ qc, const uint32_t* __restrict__ qs,
     float* __restrict__ scores, uint32_t* __restrict__ ham) {
-    __shared__ float qsum[kMaxGroup * 8];
     __shared__ float cb[16];
     const uint32_t row = blockIdx.y;
     const size_t qrow0 = (size_t)row * group;
-    stage_codebook(cb);
-    if constexpr (!EXACT) stage_qsum(qc, qrow0, group, qsum);
-    __syncthreads();
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n_tok) return;
+    const bool valid = t < n_tok;
     uint32_t w[32];
-    load_tile(tiles + ((size_t)row * n_tok + t) * 8, w);
-    score_dispatch<EXACT, HAM>(w, group, qrow0, qc, qs, cb, qsum, scores + qrow0 * n_tok,
+    if (valid) load_tile(tiles + ((size_t)row * n_tok + t) * 8, w);
+    stage_codebook(cb);
+    __syncthreads();
+    if (!valid) return;
+    score_dispatch<EXACT, HAM>(w, group, qrow0, qc, qs, cb, scores + qrow0 * n_tok,
                                HAM ? ham + qrow0 * n_tok : nullptr, n_tok, t);
+}
+
+// Fast scoring of tile rows on the matrix cores (group <= kMfmaMaxGroup).
+// Each wave fetches its 64 tiles with coalesced loads (fetch_tiles_*). With
+// REG_STAGE (group <= kRegStageMaxGroup) the query loads are issued first and
+// the tile loads stay in flight across the workgroup barrier.
+template <uint32_t REG_ROWS>
+__global__ __launch_bounds__(256) void score_rows_fast_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float cb[16];
+    __shared__ uint4 tile_lds[4][512];  // one 8 KiB region per wave
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // staging_bytes(group)
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const StagedQueries sq = carve_staging(qlds, REG_ROWS ? REG_ROWS : staging_rows(group));
+    QueryRegs<REG_ROWS ? REG_ROWS : 4> qr;
+    if constexpr (REG_ROWS > 0) stage_issue<REG_ROWS>(qc, qrow0, group, qr);
+    const uint32_t wave0 = blockIdx.x * blockDim.x + (threadIdx.x & ~63u);
+    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    uint4 v[8];
+    // A wave entirely past the row re-reads the row's first tile (n_tok >= 1).
+    fetch_tiles_issue(tiles + ((size_t)row * n_tok + (n_valid ? wave0 : 0u)) * 8, n_valid ? n_valid : 1u, v);
+    stage_codebook(cb);
+    if constexpr (REG_ROWS > 0) {
+        stage_commit<REG_ROWS>(qr, group, sq);
+        lds_barrier();
+    } else {
+        stage_queries(qc, qrow0, group, sq.q32);
+        stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
+        __syncthreads();
+    }
+    fetch_tiles_mask(n_valid, v);
+    uint32_t w[32];
+    fetch_tiles_transpose(v, tile_lds[threadIdx.x >> 6], w);
+    const bool valid = t < n_tok;
+    float* out = scores + qrow0 * n_tok;
+    if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, n_tok, t))
+        return;
+    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
+}
+
+// Persistent, double-buffered fast scoring of tile rows. Block (x, row) owns
+// batches_per_wave consecutive 64-tile batches per wave; wave w of the block
+// takes batches (x*B + k)*4 + w, k = 0..B-1, so the four waves of a block
+// walk one contiguous stretch of the row together. Each wave issues the loads
+// of batch k+1 before it decodes and scores batch k: the memory stream keeps
+// flowing while the matrix cores work, and only the last batch's compute is
+// exposed at the end of the kernel.
+__device__ __forceinline__ void load_tile_or_zero(const uint4* __restrict__ rowp, uint32_t t,
+                                                  uint32_t n_tok, uint32_t* w) {
+    if (t < n_tok) {
+        load_tile(rowp + (size_t)t * 8, w);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = 0u;
+    }
+}
+
+__device__ __forceinline__ void score_batch_fast(const uint32_t* w, uint32_t t, uint32_t n_tok,
+                                                 uint32_t group, size_t qrow0,
+                                                 const StagedQueries& sq, const float* cb,
+                                                 const float* __restrict__ qc,
+                                                 const uint32_t* __restrict__ qs,
+                                                 float* __restrict__ out) {
+    const bool valid = t < n_tok;
+    if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, n_tok, t))
+        return;
+    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
+}
+
+__global__ __launch_bounds__(256) void score_rows_pipe_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores,
+    uint32_t batches_per_wave) {
+    __shared__ float cb[16];
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // staged_rows * kQStride
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t B = batches_per_wave;
+    const uint32_t first = blockIdx.x * B * 4u + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint4* rowp = tiles + (size_t)row * n_tok * 8;
+    float* out = scores + qrow0 * n_tok;
+    uint32_t wa[32], wb[32];
+    load_tile_or_zero(rowp, first * 64u + lane, n_tok, wa);
+    stage_codebook(cb);
+    const StagedQueries sq = carve_staging(qlds, staging_rows(group));
+    stage_queries(qc, qrow0, group, sq.q32);
+    stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
+    __syncthreads();
+    for (uint32_t k = 0; k < B; k += 2) {
+        const uint32_t ta = (first + 4u * k) * 64u + lane;
+        const uint32_t tb = ta + 256u;
+        if (k + 1 < B) load_tile_or_zero(rowp, tb, n_tok, wb);
+        score_batch_fast(wa, ta, n_tok, group, qrow0, sq, cb, qc, qs, out);
+        if (k + 1 < B) {
+            if (k + 2 < B) load_tile_or_zero(rowp, tb + 256u, n_tok, wa);
+            score_batch_fast(wb, tb, n_tok, group, qrow0, sq, cb, qc, qs, out);
+        }
+    }
 }
 
 // CCOS paged scoring: block (x, y) covers tokens [256x, 256x+256) of
@@ -294,24 +741,38 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
     uint32_t max_pages, const uint32_t* __restrict__ seq_len,
     const unsigned long long* __restrict__ score_base, uint32_t n_kv, uint32_t group,
     const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
-    __shared__ float qsum[kMaxGroup * 8];
     __shared__ float cb[16];
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // staged_rows * kQStride
     const uint32_t y = blockIdx.y;
     const uint32_t s = y / n_kv, h = y - s * n_kv;
     const uint32_t len = seq_len[s];
     if (blockIdx.x * blockDim.x >= len) return;  // whole block past this sequence
     const size_t qrow0 = (size_t)y * group;
-    stage_codebook(cb);
-    stage_qsum(qc, qrow0, group, qsum);
-    __syncthreads();
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= len) return;
-    const uint32_t phys = page_table[(size_t)y * max_pages + (t >> page_shift)];
-    const size_t slot = ((size_t)phys << page_shift) + (t & ((1u << page_shift) - 1u));
+    const bool valid = t < len;
     uint32_t w[32];
-    load_tile(arena + slot * 8, w);
+    if (valid) {
+        const uint32_t phys = page_table[(size_t)y * max_pages + (t >> page_shift)];
+        const size_t slot = ((size_t)phys << page_shift) + (t & ((1u << page_shift) - 1u));
+        load_tile(arena + slot * 8, w);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = 0u;
+    }
+    stage_codebook(cb);
+    const bool mfma = group <= kMfmaMaxGroup;
+    const StagedQueries sq = carve_staging(qlds, staging_rows(group));
+    if (mfma) {
+        stage_queries(qc, qrow0, group, sq.q32);
+        stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
+    }
+    __syncthreads();
     float* out = scores + score_base[s] + (size_t)h * group * len;
-    score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, qsum, out, nullptr, len, t);
+    if (mfma && score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out,
+                                    len, t))
+        return;
+    if (!valid) return;
+    score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, len, t);
 }
 
 // ---------------------------------------------------------------------------
@@ -918,17 +1379,30 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
     if (n_rows == 0 || n_tok == 0 || group == 0) return hipSuccess;
     dim3 grid((n_tok + 255) / 256, n_rows);
     const uint4* tp = static_cast<const uint4*>(tiles);
+    const size_t smem =
+        (!exact && !ham && group <= kMfmaMaxGroup) ? staging_bytes(staging_rows(group)) : 0;
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
+    if (!exact && !ham && group <= kMfmaMaxGroup) {
+        if (group <= 4)
+            score_rows_fast_kernel<4><<<grid, 256, staging_bytes(4), s>>>(tp, n_tok, group, qc,
+                                                                           qsw, scores);
+        else if (group <= kRegStageMaxGroup)
+            score_rows_fast_kernel<16><<<grid, 256, staging_bytes(16), s>>>(tp, n_tok, group, qc,
+                                                                             qsw, scores);
+        else
+            score_rows_fast_kernel<0><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores);
+        return hipGetLastError();
+    }
     if (exact) {
         if (ham)
-            score_rows_kernel<true, true><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+            score_rows_kernel<true, true><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
         else
-            score_rows_kernel<true, false><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+            score_rows_kernel<true, false><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
     } else {
         if (ham)
-            score_rows_kernel<false, true><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+            score_rows_kernel<false, true><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
         else
-            score_rows_kernel<false, false><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
+            score_rows_kernel<false, false><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
     }
     return hipGetLastError();
 }
@@ -942,7 +1416,8 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
     if (n_seq == 0 || max_len == 0) return hipSuccess;
     const auto* base = reinterpret_cast<const unsigned long long*>(score_base);
     dim3 grid((max_len + 255) / 256, n_seq * n_kv);
-    score_paged_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(arena), page_shift,
+    const size_t smem = group <= kMfmaMaxGroup ? staging_bytes(staging_rows(group)) : 0;
+    score_paged_kernel<<<grid, 256, smem, s>>>(static_cast<const uint4*>(arena), page_shift,
                                             page_table, max_pages, seq_len, base, n_kv, group, qc,
                                             reinterpret_cast<const uint32_t*>(qs), scores);
     hipError_t e = hipGetLastError();
