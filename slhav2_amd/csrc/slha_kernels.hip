@@ -672,67 +672,6 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
-// Persistent, double-buffered fast scoring of tile rows. Block (x, row) owns
-// batches_per_wave consecutive 64-tile batches per wave; wave w of the block
-// takes batches (x*B + k)*4 + w, k = 0..B-1, so the four waves of a block
-// walk one contiguous stretch of the row together. Each wave issues the loads
-// of batch k+1 before it decodes and scores batch k: the memory stream keeps
-// flowing while the matrix cores work, and only the last batch's compute is
-// exposed at the end of the kernel.
-__device__ __forceinline__ void load_tile_or_zero(const uint4* __restrict__ rowp, uint32_t t,
-                                                  uint32_t n_tok, uint32_t* w) {
-    if (t < n_tok) {
-        load_tile(rowp + (size_t)t * 8, w);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) w[i] = 0u;
-    }
-}
-
-__device__ __forceinline__ void score_batch_fast(const uint32_t* w, uint32_t t, uint32_t n_tok,
-                                                 uint32_t group, size_t qrow0,
-                                                 const StagedQueries& sq, const float* cb,
-                                                 const float* __restrict__ qc,
-                                                 const uint32_t* __restrict__ qs,
-                                                 float* __restrict__ out) {
-    const bool valid = t < n_tok;
-    if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, n_tok, t))
-        return;
-    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
-}
-
-__global__ __launch_bounds__(256) void score_rows_pipe_kernel(
-    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
-    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores,
-    uint32_t batches_per_wave) {
-    __shared__ float cb[16];
-    extern __shared__ __attribute__((aligned(16))) float qlds[];  // staged_rows * kQStride
-    const uint32_t row = blockIdx.y;
-    const size_t qrow0 = (size_t)row * group;
-    const uint32_t B = batches_per_wave;
-    const uint32_t first = blockIdx.x * B * 4u + (threadIdx.x >> 6);
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint4* rowp = tiles + (size_t)row * n_tok * 8;
-    float* out = scores + qrow0 * n_tok;
-    uint32_t wa[32], wb[32];
-    load_tile_or_zero(rowp, first * 64u + lane, n_tok, wa);
-    stage_codebook(cb);
-    const StagedQueries sq = carve_staging(qlds, staging_rows(group));
-    stage_queries(qc, qrow0, group, sq.q32);
-    stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
-    __syncthreads();
-    for (uint32_t k = 0; k < B; k += 2) {
-        const uint32_t ta = (first + 4u * k) * 64u + lane;
-        const uint32_t tb = ta + 256u;
-        if (k + 1 < B) load_tile_or_zero(rowp, tb, n_tok, wb);
-        score_batch_fast(wa, ta, n_tok, group, qrow0, sq, cb, qc, qs, out);
-        if (k + 1 < B) {
-            if (k + 2 < B) load_tile_or_zero(rowp, tb + 256u, n_tok, wa);
-            score_batch_fast(wb, tb, n_tok, group, qrow0, sq, cb, qc, qs, out);
-        }
-    }
-}
-
 // CCOS paged scoring: block (x, y) covers tokens [256x, 256x+256) of
 // (sequence s, KV head h) with y = s*n_kv + h; token t lives in physical page
 // page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.

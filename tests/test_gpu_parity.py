@@ -149,6 +149,36 @@ def test_score_exact_bit_identical_and_hamming(s, torch, group):
             assert_tol(fast[qi], ref)
 
 
+@pytest.mark.parametrize("group,codec", [(4, 0), (8, 2), (20, 4), (5, None)])
+def test_score_fast_streaming_ragged(s, torch, group, codec):
+    # Enough 64-tile batches that every wave of the fast kernel streams several
+    # of them, with a ragged last batch per row (n_tok not a multiple of 64)
+    # and batches past the end of the row. codec None: random mixed-codec
+    # tiles, so waves fall back to the per-lane path inside the stream loop.
+    n_rows, n_tok = 8, 50_001
+    r = np.random.default_rng(1000 + group)
+    if codec is None:
+        td = dev(torch, random_tiles(n_rows * n_tok, 7).view(np.uint8).reshape(n_rows, n_tok, 128))
+    else:
+        g = torch.Generator(device="cuda").manual_seed(group)
+        keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
+        with s.Model(seed=group) as m:
+            td = s.gpu_encode(m, keys, codec, n_kv_heads=n_rows)
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
+    qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
+    fast = s.gpu_score(td, qd, qsd, group=group).cpu().numpy()
+    exact = s.gpu_score(td, qd, qsd, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+    assert_tol(fast, exact)
+    tn = tiles_np(td)
+    for row in (0, n_rows - 1):
+        idx = np.r_[0:70, n_tok - 70:n_tok]
+        qi = row * group + group - 1
+        ref, _ = o.score(tn[row * n_tok + idx], q[qi], qs[qi])
+        assert np.array_equal(exact[qi, idx].view(np.uint32), ref.view(np.uint32))
+        assert_tol(fast[qi, idx], ref)
+
+
 def test_score_fast_wide_group_c4_shape(s, torch):
     # C4 shape: one row, 64 queries per tile (TQ3 + RHT tiles).
     keys = keys_for(99, 2048, "scaled")
