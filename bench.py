@@ -13,8 +13,12 @@ round-robin, so a step never finds its tiles in the 256 MiB MALL.
 Prints ONE JSON line. value = query-tile pairs scored per second over the timed
 steps; roofline.achieved = algorithmic bytes per launch / mean kernel duration,
 the latter from HIP events bracketing the timed region on the launch stream
-(one kernel per step, launched back to back); cpu_baseline = the AVX-512/AVX2
-restatement of the reference's compute_score, timed on this host.
+(one kernel per step, launched back to back through the C ABI with prebuilt
+arguments, so the host keeps ahead of the GPU); roofline.traffic = HBM bytes per
+launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, scaled by the
+same counters' reading for a plain copy kernel (--copy-calibration runs that
+copy); cpu_baseline = the AVX-512/AVX2 restatement of the reference's
+compute_score, timed on this host.
 """
 from __future__ import annotations
 
@@ -36,6 +40,35 @@ PAIRS = N_Q * N_TOK
 ROTATION = 10
 PEAK_HBM_GBS = 8000.0
 TILE_BYTES = 128
+SCORE_KERNEL = "slha::score_rows_fast_kernel<4u>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "score_rows_fast_kernel_c2_traffic.txt"
+COPY_BYTES = 1 << 30
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per score launch from the committed counter summary, if any."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_calibration() -> int:
+    """A plain device copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES),
+    launched 5 times: the reference reading for FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 5}), flush=True)
+    return 0
 
 
 def algorithmic_bytes() -> int:
@@ -97,12 +130,17 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the plain copy used to calibrate HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the hot path shards by (sequence, KV head) with no exchange; see DESIGN.md)",
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the scoring hot path shards by (sequence, KV head) with no exchange "
+              "between GPUs, so N GPUs would each run this same per-GPU step)",
               file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
 
     import torch
 
@@ -137,9 +175,25 @@ def main() -> int:
     torch.cuda.synchronize()
     enc_ms = e0.elapsed_time(e1) / n_enc
 
+    # Steps call the C ABI directly with prebuilt arguments (the Python
+    # wrapper's checks cost about as much host time as the kernel itself).
+    score = s.lib.slha_gpu_score
+    vp = ctypes.c_void_p
+    sargs = [(vp(sets[k].data_ptr()), N_KV, N_TOK, vp(qc.data_ptr()), vp(qs.data_ptr()), GROUP,
+              s.SCORE_FAST, vp(outs[k].data_ptr()), None, vp(stream.cuda_stream))
+             for k in range(ROTATION)]
+
     def step(i: int) -> None:
-        k = i % ROTATION
-        s.gpu_score(sets[k], qc, qs, group=GROUP, out=outs[k], stream=stream)
+        rc = score(*sargs[i % ROTATION])
+        if rc != 0:
+            raise RuntimeError(f"slha_gpu_score failed: {rc} {s.last_error()}")
+
+    # the fast path of the C ABI must agree with the Python wrapper
+    ref = s.gpu_score(sets[0], qc, qs, group=GROUP, stream=stream)
+    step(0)
+    torch.cuda.synchronize()
+    if not torch.equal(ref, outs[0]):
+        raise RuntimeError("direct C-ABI launch disagrees with gpu_score")
 
     for i in range(args.warmup):
         step(i)
@@ -186,8 +240,8 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
-            "traffic": None,
-            "kernel": "slha::score_rows_kernel<false,false>",
+            "traffic": measured_traffic(),
+            "kernel": SCORE_KERNEL,
             "algorithmic_bytes_per_launch": nbytes,
             "kernel_ms": kern_ms,
         },

@@ -33,8 +33,13 @@ HIPCC_FLAGS = [
     # Rust never contracts a*b+c; exact kernels rely on this. Fast kernels
     # call fmaf() explicitly.
     "-ffp-contract=off",
-    # Keep hipcc away from packed-FP32 instructions.
+    # Keep hipcc away from packed-FP32 instructions (v_pk_add/mul/fma_f32):
+    # some of their forms have given sporadic wrong results on these GPUs.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs rather than AGPRs: the score kernels read every
+    # accumulator back with VALU, and AGPRs would cost a copy per register
+    # and one wave of occupancy.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

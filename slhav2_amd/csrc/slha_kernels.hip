@@ -236,6 +236,11 @@ __device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group,
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 constexpr uint32_t kQStride = 132;      // LDS row stride of a staged query (floats)
 constexpr uint32_t kQStrideH = 264;     // u16 words per staged f16 query (512 B + 16 B pad)
 constexpr uint32_t kMfmaMaxGroup = 64;  // queries staged in LDS per workgroup
@@ -315,24 +320,27 @@ __device__ __forceinline__ void score_wave_mfma(const uint32_t* w_in, bool valid
 }
 
 // INT4 fast path on v_mfma_f32_4x4x4_16b_f16 (same lane = tile layout,
-// four dims per MFMA). B is the exact integer (n - 8) * gs in f16
-// (|.| <= 2040 < 2^11), built from magic-number halves: for a latent dword x
-// holding nibbles n0..n7, (x & 0x000F000F) | 0x64006400 is the f16 pair
-// (1024 + n0, 1024 + n4) and (x & 0x00F000F0) | 0x64006400 is
-// (1024 + 16 n1, 1024 + 16 n5); one packed add / fma recovers n - 8 exactly
-// and one packed mul applies gs. The dims of a dword therefore enter the
-// MFMA in the order (d0, d4, d1, d5 | d2, d6, d3, d7), and the staged
-// queries use the same order. Each query is prescaled by an exact power of
+// four dims per MFMA). B is the exact integer n - 8 in f16, built from
+// magic-number halves: for a latent dword x holding nibbles n0..n7,
+// (x & 0x000F000F) | 0x64006400 is the f16 pair (1024 + n0, 1024 + n4) and
+// (x & 0x00F000F0) | 0x64006400 is (1024 + 16 n1, 1024 + 16 n5); one
+// v_and_or_b32 plus one packed add / fma per pair gives n - 8 exactly. The
+// dims of a dword therefore enter the MFMA in the order
+// (d0, d4, d1, d5 | d2, d6, d3, d7), and the staged queries use the same
+// order. Each 16-dim group is accumulated on its own and then added in with
+// its group scale gs, once per (tile, query, group) instead of once per
+// element. Each query is prescaled by an exact power of
 // two 2^-e (|q 2^-e| <= 1) and split into f16 hi + lo halves, so q is carried
-// to ~2^-22 relative and every product is exact in the f32 accumulator. The
+// to ~2^-20 relative and every product is exact in the f32 accumulator. The
 // tile's scale/255 and 2^e are applied once per (tile, query) at the end.
 
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
-
 __device__ __forceinline__ v2h as_v2h(uint32_t u) { return __builtin_bit_cast(v2h, u); }
 
+// ONE_CHUNK: group <= 4, a single pass with no loop-carried copy of the tile.
+template <bool ONE_CHUNK>
 __device__ __forceinline__ void score_wave_int4_f16(const uint32_t* w_in, bool valid,
                                                     uint32_t group, size_t qrow0,
                                                     const uint16_t* qh, const float* qexp,
@@ -343,40 +351,51 @@ __device__ __forceinline__ void score_wave_int4_f16(const uint32_t* w_in, bool v
     const v2h k_lo = v2h{(_Float16)-1032.0f, (_Float16)-1032.0f};
     const v2h k_sixteenth = v2h{(_Float16)0.0625f, (_Float16)0.0625f};
     const v2h k_hi = v2h{(_Float16)-72.0f, (_Float16)-72.0f};
+    // Held in a VGPR: a VOP3 op reads at most one SGPR or literal here, and
+    // the masks take that slot in v_and_or_b32.
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    uint32_t w[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) w[i] = w_in[i];
 #pragma unroll 1
     for (uint32_t c0 = 0; c0 < group; c0 += 4) {
-        uint32_t w[32];
+        // Opaque per chunk: keeps the decode inside the loop (see score_lane).
+        if constexpr (!ONE_CHUNK) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            w[i] = w_in[i];
-            asm volatile("" : "+v"(w[i]));
+            for (int i = 0; i < 32; ++i) asm volatile("" : "+v"(w[i]));
         }
         const uint16_t* qa = qh + (c0 + r) * kQStrideH;
-        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        v4f dot = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int p = 0; p < 16; ++p) {
-            const float gsf = gs_at(w + 30, p >> 1);
-            const v2h gs2 = v2h{(_Float16)gsf, (_Float16)gsf};
-            const uint32_t x = w[p];
-            const uint32_t x8 = x >> 8;
-            const v2h l0 = (as_v2h((x & 0x000F000Fu) | 0x64006400u) + k_lo) * gs2;
-            const v2h l1 = __builtin_elementwise_fma(as_v2h((x & 0x00F000F0u) | 0x64006400u),
-                                                     k_sixteenth, k_hi) * gs2;
-            const v2h l2 = (as_v2h((x8 & 0x000F000Fu) | 0x64006400u) + k_lo) * gs2;
-            const v2h l3 = __builtin_elementwise_fma(as_v2h((x8 & 0x00F000F0u) | 0x64006400u),
-                                                     k_sixteenth, k_hi) * gs2;
-            const v4h b01 = v4h{l0.x, l0.y, l1.x, l1.y};
-            const v4h b23 = v4h{l2.x, l2.y, l3.x, l3.y};
-            const uint4 hq = *reinterpret_cast<const uint4*>(qa + 16 * p);      // hi halves
-            const uint4 lq = *reinterpret_cast<const uint4*>(qa + 16 * p + 8);  // lo halves
-            const v4h a_hi01 = __builtin_bit_cast(v4h, make_uint2(hq.x, hq.y));
-            const v4h a_hi23 = __builtin_bit_cast(v4h, make_uint2(hq.z, hq.w));
-            const v4h a_lo01 = __builtin_bit_cast(v4h, make_uint2(lq.x, lq.y));
-            const v4h a_lo23 = __builtin_bit_cast(v4h, make_uint2(lq.z, lq.w));
-            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi01, b01, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo01, b01, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi23, b23, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo23, b23, acc, 0, 0, 0);
+        for (int g = 0; g < 8; ++g) {
+            v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 2 * g; p < 2 * g + 2; ++p) {
+                const uint32_t x = w[p];
+                const uint32_t x8 = x >> 8;
+                const v2h l0 = as_v2h((x & 0x000F000Fu) | magic) + k_lo;
+                const v2h l1 = __builtin_elementwise_fma(as_v2h((x & 0x00F000F0u) | magic),
+                                                         k_sixteenth, k_hi);
+                const v2h l2 = as_v2h((x8 & 0x000F000Fu) | magic) + k_lo;
+                const v2h l3 = __builtin_elementwise_fma(as_v2h((x8 & 0x00F000F0u) | magic),
+                                                         k_sixteenth, k_hi);
+                const v4h b01 = v4h{l0.x, l0.y, l1.x, l1.y};
+                const v4h b23 = v4h{l2.x, l2.y, l3.x, l3.y};
+                const uint4 hq = *reinterpret_cast<const uint4*>(qa + 16 * p);      // hi halves
+                const uint4 lq = *reinterpret_cast<const uint4*>(qa + 16 * p + 8);  // lo halves
+                const v4h a_hi01 = __builtin_bit_cast(v4h, make_uint2(hq.x, hq.y));
+                const v4h a_hi23 = __builtin_bit_cast(v4h, make_uint2(hq.z, hq.w));
+                const v4h a_lo01 = __builtin_bit_cast(v4h, make_uint2(lq.x, lq.y));
+                const v4h a_lo23 = __builtin_bit_cast(v4h, make_uint2(lq.z, lq.w));
+                acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi01, b01, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo01, b01, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_hi23, b23, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_4x4x4f16(a_lo23, b23, acc, 0, 0, 0);
+            }
+            const float gsf = gs_at(w + 30, g);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) dot[rr] = fmaf(acc[rr], gsf, dot[rr]);
         }
         const float s255 = __uint_as_float(w[24]) * (1.0f / 255.0f);
         const float lambda = __uint_as_float(w[25]);
@@ -384,12 +403,13 @@ __device__ __forceinline__ void score_wave_int4_f16(const uint32_t* w_in, bool v
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             if (c0 + rr < group) {
-                float sc = acc[rr] * (s255 * qexp[c0 + rr]);
+                float sc = dot[rr] * (s255 * qexp[c0 + rr]);
                 const uint32_t h = hamming_words(w + 16, qs + (qrow0 + c0 + rr) * 8);
                 if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
                 if (valid) out[(size_t)(c0 + rr) * stride + t] = sc;
             }
         }
+        if constexpr (ONE_CHUNK) break;
     }
 }
 
@@ -410,7 +430,10 @@ __device__ __forceinline__ bool score_wave_try_mfma(const uint32_t* w, bool vali
     const int c0 = __builtin_amdgcn_readfirstlane(cls);
     if (c0 < 0 || !__all(cls == c0 || cls < 0)) return false;
     if (c0 == kClsInt4 && qh) {
-        score_wave_int4_f16(w, valid, group, qrow0, qh, qexp, qs, out, stride, t);
+        if (group <= 4)
+            score_wave_int4_f16<true>(w, valid, group, qrow0, qh, qexp, qs, out, stride, t);
+        else
+            score_wave_int4_f16<false>(w, valid, group, qrow0, qh, qexp, qs, out, stride, t);
         return true;
     }
 #define SLHA_WAVE(C) score_wave_mfma<C>(w, valid, group, qrow0, qlds, cb, qs, out, stride, t)
@@ -440,6 +463,31 @@ __device__ __forceinline__ void stage_queries(const float* __restrict__ qc, size
     }
 }
 
+// Max over the wave of non-negative floats (their IEEE order is their bit
+// order): DPP quad, half-row and row mirrors, then row broadcasts 15 and 31
+// leave the maximum in lane 63.
+__device__ __forceinline__ float wave_max_nonneg(float m) {
+    int v = (int)__float_as_uint(m);
+    // Full-row patterns read a valid lane everywhere; the broadcasts leave
+    // lanes outside their row mask at 0, the identity of this max.
+#define SLHA_DPP_MAX(ctrl, rows) \
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, ctrl, rows, 0xF, false))
+    SLHA_DPP_MAX(0xB1, 0xF);   // quad_perm [1,0,3,2]
+    SLHA_DPP_MAX(0x4E, 0xF);   // quad_perm [2,3,0,1]
+    SLHA_DPP_MAX(0x141, 0xF);  // row_half_mirror
+    SLHA_DPP_MAX(0x140, 0xF);  // row_mirror
+    SLHA_DPP_MAX(0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    SLHA_DPP_MAX(0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+#undef SLHA_DPP_MAX
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane(v, 63));
+}
+
+// Dims a lane stages for the f16 path: (d, d + 4) with d = 8 (lane/4) + lane%4,
+// which sit next to each other in the (d0, d4, d1, d5, d2, d6, d3, d7) order.
+__device__ __forceinline__ uint32_t f16_stage_dim(uint32_t lane) {
+    return 8u * (lane >> 2) + (lane & 3u);
+}
+
 // Two-phase query staging for group <= kRegStageMaxGroup: stage_issue() only
 // issues the global loads into registers, so the kernel can issue its tile
 // loads right after them; stage_commit() then waits for the (older) query
@@ -452,53 +500,59 @@ constexpr uint32_t kRegStageMaxGroup = 16;
 template <uint32_t ROWS>
 struct QueryRegs {
     float4 a[ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1];  // f32 copy, float4 (threadIdx.x + 256 k) mod 32*ROWS
-    float2 b[ROWS / 4];                                  // f16 copy: row wave + 4 k
+    float2 b[ROWS / 4];  // f16 copy: row wave + 4 k, dims (d, d + 4), d = f16_stage_dim(lane)
 };
 
 template <uint32_t ROWS>
 __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t qrow0,
                                             uint32_t group, QueryRegs<ROWS>& r) {
-    // Branch-free (clamped rows, zeroed in stage_commit) for exact wait counts.
+    // Buffer loads over exactly the row's `group` queries: rows past `group`
+    // fall outside the range and read as zero, with no branch or clamp.
     constexpr uint32_t NA = ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1;
-    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t bytes =
+        __builtin_amdgcn_readfirstlane((group < ROWS ? group : ROWS) * kDC * 4u);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(qc + qrow0 * kDC), 0, bytes, 0x00020000);
 #pragma unroll
     for (uint32_t k = 0; k < NA; ++k) {
-        const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u), q = i >> 5;
-        const uint32_t qq = q < group ? q : group - 1u;
-        r.a[k] = reinterpret_cast<const float4*>(qc + (qrow0 + qq) * kDC)[i & 31u];
+        const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u);  // float4 index
+        r.a[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16u * i, 0, 0));
     }
+    const uint32_t voff = 4u * f16_stage_dim(lane);
 #pragma unroll
     for (uint32_t k = 0; k < ROWS / 4; ++k) {
-        const uint32_t j = wv + 4u * k;
-        const uint32_t jj = j < group ? j : group - 1u;
-        r.b[k] = reinterpret_cast<const float2*>(qc + (qrow0 + jj) * kDC)[lane];
+        const uint32_t soff = (wv + 4u * k) * kDC * 4u;
+        r.b[k] = make_float2(
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, soff, 0)),
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff + 16u, soff, 0)));
     }
 }
 
+// v0 = q_j[d], v1 = q_j[d + 4] with d = f16_stage_dim(lane); one wave per query.
 __device__ __forceinline__ void stage_f16_row(float v0, float v1, uint32_t j, uint16_t* qh,
                                               float* qexp) {
     const uint32_t lane = threadIdx.x & 63u;
-    float m = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float m = wave_max_nonneg(fmaxf(fabsf(v0), fabsf(v1)));
     int e = 0;  // smallest power of two >= m (m = 0 -> 1)
     if (m > 0.0f) {
         (void)frexpf(m, &e);
         if (ldexpf(1.0f, e - 1) == m) e -= 1;
     }
     const float inv = ldexpf(1.0f, -e);
-    const float d[2] = {v0 * inv, v1 * inv};
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const uint32_t dim = 2 * lane + k;
-        const _Float16 hi = (_Float16)d[k];
-        const _Float16 lo = (_Float16)(d[k] - (float)hi);
-        // position of dim inside its dword's (d0, d4, d1, d5, d2, d6, d3, d7) order
-        const uint32_t n = dim & 7u, pword = dim >> 3;
-        const uint32_t slot = (n & 1u ? 2u : 0u) + (n >> 2) + (n & 2u ? 4u : 0u);
-        qh[j * kQStrideH + 16 * pword + slot] = __builtin_bit_cast(uint16_t, hi);
-        qh[j * kQStrideH + 16 * pword + 8 + slot] = __builtin_bit_cast(uint16_t, lo);
-    }
+    const float d0 = v0 * inv, d1 = v1 * inv;
+    // Truncating f16 split: x - hi is exact in f32 and lo keeps 11 more bits.
+    const auto hi = __builtin_amdgcn_cvt_pkrtz(d0, d1);
+    const auto lo = __builtin_amdgcn_cvt_pkrtz(d0 - (float)hi.x, d1 - (float)hi.y);
+    const uint32_t n = lane & 3u, pword = lane >> 2;
+    // Stored from inline asm: the compiler would merge two plain stores into
+    // one ds_write2_b32, which loses the information that they do not alias
+    // the tile regions the DMA loads fill, and then wait for those loads.
+    const uint32_t addr = lds_byte_addr(qh + j * kQStrideH + 16 * pword + 2 * n);
+    asm volatile("ds_write_b32 %0, %1\n\tds_write_b32 %0, %2 offset:16" ::"v"(addr),
+                 "v"(__builtin_bit_cast(uint32_t, hi)), "v"(__builtin_bit_cast(uint32_t, lo))
+                 : "memory");
     if (lane == 0) qexp[j] = ldexpf(1.0f, e);
 }
 
@@ -507,15 +561,18 @@ __device__ __forceinline__ void stage_queries_f16(const float* __restrict__ qc, 
     const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t rows = (group + 3u) & ~3u;
     for (uint32_t j = wv; j < rows; j += nw) {
-        float2 v = make_float2(0.0f, 0.0f);
-        if (j < group) v = reinterpret_cast<const float2*>(qc + (qrow0 + j) * kDC)[lane];
-        stage_f16_row(v.x, v.y, j, qh, qexp);
+        float v0 = 0.0f, v1 = 0.0f;
+        if (j < group) {
+            const float* q = qc + (qrow0 + j) * kDC + f16_stage_dim(lane);
+            v0 = q[0];
+            v1 = q[4];
+        }
+        stage_f16_row(v0, v1, j, qh, qexp);
     }
 }
 
-// Writes all ROWS staged rows (rows past `group` are zero; threads past
-// 32*ROWS float4s rewrite identical values), so no branch disturbs the
-// vector-memory wait counts.
+// Writes all ROWS staged rows (rows past `group` were read as zero; threads
+// past 32*ROWS float4s rewrite identical values), with no branch.
 template <uint32_t ROWS>
 __device__ __forceinline__ void stage_commit(const QueryRegs<ROWS>& r, uint32_t group,
                                              const StagedQueries& sq) {
@@ -524,18 +581,11 @@ __device__ __forceinline__ void stage_commit(const QueryRegs<ROWS>& r, uint32_t 
 #pragma unroll
     for (uint32_t k = 0; k < NA; ++k) {
         const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u), q = i >> 5;
-        const float m = q < group ? 1.0f : 0.0f;  // value select: no pointer select
-        const float4 x = r.a[k];
-        *reinterpret_cast<float4*>(sq.q32 + q * kQStride + 4 * (i & 31u)) =
-            make_float4(x.x * m, x.y * m, x.z * m, x.w * m);
+        *reinterpret_cast<float4*>(sq.q32 + q * kQStride + 4 * (i & 31u)) = r.a[k];
     }
 #pragma unroll
-    for (uint32_t k = 0; k < ROWS / 4; ++k) {
-        const uint32_t j = wv + 4u * k;
-        const float m = j < group ? 1.0f : 0.0f;
-        const float2 x = r.b[k];
-        stage_f16_row(x.x * m, x.y * m, j, sq.q16, sq.qexp);
-    }
+    for (uint32_t k = 0; k < ROWS / 4; ++k)
+        stage_f16_row(r.b[k].x, r.b[k].y, wv + 4u * k, sq.q16, sq.qexp);
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -563,43 +613,36 @@ __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group
 #undef SLHA_LANE
 }
 
-// Coalesced tile fetch for a wave's 64 consecutive tiles (8 KiB): load j of
-// lane l reads the 16 B at byte 1024 j + 16 l, so every load instruction of the
-// wave covers 1 KiB of contiguous HBM, and writes it to a wave-private LDS
-// region; lane l then reads back tile l. Chunk c of tile u sits at uint4
-// slot 8u + (c ^ (u & 7)): the XOR swizzle keeps both the writes and the
-// lane-per-tile reads free of bank conflicts. Tiles at or past n_valid read
-// as zero. Only lanes of one wave touch the region, so no barrier is needed.
-__device__ __forceinline__ void fetch_tiles_issue(const uint4* __restrict__ base, uint32_t n_valid,
-                                                  uint4* v) {
-    // Branch-free: out-of-range lanes re-read uint4 0 of the wave's first
-    // tile (always valid: the caller passes n_valid >= 1) and are zeroed when
-    // the data arrives, so the wait counters stay exact.
+// Coalesced direct-to-LDS fetch of a wave's 64 consecutive tiles (8 KiB)
+// into its LDS region. buffer_load_dwordx4 ... lds writes lane l of load j to
+// region + 1024 j + 16 l; each lane picks the global chunk that belongs in
+// that slot under the swizzle "chunk c of tile u at uint4 slot
+// 8u + (c ^ (u & 7))", so every load instruction reads 1 KiB of contiguous
+// HBM (8 lanes per 128-B tile, chunks permuted inside the tile) and no VGPRs
+// hold the data in flight. The buffer's range ends at the last valid tile:
+// slots of tiles at or past n_valid read as zero. The compiler waits for
+// these loads (vmcnt) before the region is read back.
+__device__ __forceinline__ void fetch_tiles_lds(const uint4* wave_base, uint32_t n_valid,
+                                                uint4* region) {
     const uint32_t lane = threadIdx.x & 63u;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t idx = 64u * j + lane;  // uint4 index within the 8 KiB
-        v[j] = base[(idx >> 3) < n_valid ? idx : 0u];
-    }
-}
-
-__device__ __forceinline__ void fetch_tiles_mask(uint32_t n_valid, uint4* v) {
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t in_tile = (lane & 0x38u) + ((lane & 7u) ^ (lane >> 3));
+    // readfirstlane: the range is wave-uniform, and a descriptor built from
+    // VGPRs would be legalised into a loop over lanes.
+    const uint32_t bytes = __builtin_amdgcn_readfirstlane((n_valid < 64u ? n_valid : 64u) * 128u);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(wave_base), 0, bytes, 0x00020000);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-        if (((64u * j + lane) >> 3) >= n_valid) v[j] = make_uint4(0u, 0u, 0u, 0u);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc, (__attribute__((address_space(3))) void*)(region + 64 * j), 16, in_tile * 16u,
+            1024 * j, 0, 0);
 }
 
-__device__ __forceinline__ void fetch_tiles_transpose(const uint4* v, uint4* region, uint32_t* w) {
+// Lane l reads tile l back from a region filled by fetch_tiles_lds; the XOR
+// swizzle keeps these reads free of bank conflicts. Only lanes of one wave
+// touch the region, so no barrier is needed.
+__device__ __forceinline__ void fetch_tiles_readback(const uint4* region, uint32_t* w) {
     const uint32_t lane = threadIdx.x & 63u;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t idx = 64u * j + lane;
-        const uint32_t u = idx >> 3, c = idx & 7u;
-        region[8u * u + (c ^ (u & 7u))] = v[j];
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS writes done
-    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const uint4 x = region[8u * lane + (c ^ (lane & 7u))];
@@ -641,18 +684,23 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
     __shared__ float cb[16];
     __shared__ uint4 tile_lds[4][512];  // one 8 KiB region per wave
-    extern __shared__ __attribute__((aligned(16))) float qlds[];  // staging_bytes(group)
+    // REG_ROWS > 0: staging in a static array, so the compiler can tell that
+    // the staging stores do not touch the tile regions the DMA loads write
+    // and does not wait for those loads before them. Otherwise dynamic LDS
+    // of staging_bytes(staging_rows(group)).
+    __shared__ __attribute__((aligned(16))) float qstatic[REG_ROWS ? staging_bytes(REG_ROWS) / 4 : 1];
+    extern __shared__ __attribute__((aligned(16))) float qlds[];
     const uint32_t row = blockIdx.y;
     const size_t qrow0 = (size_t)row * group;
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    const StagedQueries sq = carve_staging(qlds, REG_ROWS ? REG_ROWS : staging_rows(group));
+    const StagedQueries sq =
+        carve_staging(REG_ROWS ? qstatic : qlds, REG_ROWS ? REG_ROWS : staging_rows(group));
     QueryRegs<REG_ROWS ? REG_ROWS : 4> qr;
     if constexpr (REG_ROWS > 0) stage_issue<REG_ROWS>(qc, qrow0, group, qr);
-    const uint32_t wave0 = blockIdx.x * blockDim.x + (threadIdx.x & ~63u);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
-    uint4 v[8];
-    // A wave entirely past the row re-reads the row's first tile (n_tok >= 1).
-    fetch_tiles_issue(tiles + ((size_t)row * n_tok + (n_valid ? wave0 : 0u)) * 8, n_valid ? n_valid : 1u, v);
+    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
     stage_codebook(cb);
     if constexpr (REG_ROWS > 0) {
         stage_commit<REG_ROWS>(qr, group, sq);
@@ -662,9 +710,8 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
         stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
         __syncthreads();
     }
-    fetch_tiles_mask(n_valid, v);
     uint32_t w[32];
-    fetch_tiles_transpose(v, tile_lds[threadIdx.x >> 6], w);
+    fetch_tiles_readback(tile_lds[wave], w);
     const bool valid = t < n_tok;
     float* out = scores + qrow0 * n_tok;
     if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, n_tok, t))
@@ -1323,11 +1370,9 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
     if (!exact && !ham && group <= kMfmaMaxGroup) {
         if (group <= 4)
-            score_rows_fast_kernel<4><<<grid, 256, staging_bytes(4), s>>>(tp, n_tok, group, qc,
-                                                                           qsw, scores);
+            score_rows_fast_kernel<4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= kRegStageMaxGroup)
-            score_rows_fast_kernel<16><<<grid, 256, staging_bytes(16), s>>>(tp, n_tok, group, qc,
-                                                                             qsw, scores);
+            score_rows_fast_kernel<16><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else
             score_rows_fast_kernel<0><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores);
         return hipGetLastError();
