@@ -4,7 +4,7 @@
  * the HIP implementation. Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it; the product library never does.
  *
- * Build: gcc -O2 -ffp-contract=off -fno-fast-math -fPIC -shared (see build.sh).
+ * Build: gcc -O2 -ffp-contract=off -fno-fast-math -fPIC -shared (slhav2_amd/build.py).
  * The -ffp-contract=off flag is load-bearing: Rust never fuses a*b+c.
  *
  * Pinning: every function is checked by tests/test_oracle.py against the
