@@ -719,8 +719,62 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
-// CCOS paged scoring: block (x, y) covers tokens [256x, 256x+256) of
-// (sequence s, KV head h) with y = s*n_kv + h; token t lives in physical page
+// CCOS paged scoring on the fast path (pages of at least 64 tiles, group <=
+// kMfmaMaxGroup): as score_rows_fast_kernel, with each wave's 64 consecutive
+// tokens gathered from one physical page. Block (x, y) covers tokens
+// [256x, 256x+256) of (sequence s, KV head h), y = s*n_kv + h; token t lives
+// in page page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
+template <uint32_t REG_ROWS>
+__global__ __launch_bounds__(256) void score_paged_fast_kernel(
+    const uint4* __restrict__ arena, uint32_t page_shift, const uint32_t* __restrict__ page_table,
+    uint32_t max_pages, const uint32_t* __restrict__ seq_len,
+    const unsigned long long* __restrict__ score_base, uint32_t n_kv, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float cb[16];
+    __shared__ uint4 tile_lds[4][512];
+    __shared__ __attribute__((aligned(16))) float qstatic[REG_ROWS ? staging_bytes(REG_ROWS) / 4 : 1];
+    extern __shared__ __attribute__((aligned(16))) float qlds[];
+    const uint32_t y = blockIdx.y;
+    const uint32_t s = y / n_kv, h = y - s * n_kv;
+    const uint32_t len = seq_len[s];
+    if (blockIdx.x * blockDim.x >= len) return;  // whole block past this sequence
+    const size_t qrow0 = (size_t)y * group;
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const StagedQueries sq =
+        carve_staging(REG_ROWS ? qstatic : qlds, REG_ROWS ? REG_ROWS : staging_rows(group));
+    QueryRegs<REG_ROWS ? REG_ROWS : 4> qr;
+    if constexpr (REG_ROWS > 0) stage_issue<REG_ROWS>(qc, qrow0, group, qr);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
+    const uint32_t n_valid = wave0 < len ? len - wave0 : 0u;
+    const uint4* base = arena;
+    if (n_valid) {  // 64 | page_tiles: the wave's tokens share one page
+        const uint32_t phys = page_table[(size_t)y * max_pages + (wave0 >> page_shift)];
+        base = arena + (((size_t)phys << page_shift) + (wave0 & ((1u << page_shift) - 1u))) * 8;
+    }
+    fetch_tiles_lds(base, n_valid, tile_lds[wave]);
+    stage_codebook(cb);
+    if constexpr (REG_ROWS > 0) {
+        stage_commit<REG_ROWS>(qr, group, sq);
+        lds_barrier();
+    } else {
+        stage_queries(qc, qrow0, group, sq.q32);
+        stage_queries_f16(qc, qrow0, group, sq.q16, sq.qexp);
+        __syncthreads();
+    }
+    uint32_t w[32];
+    fetch_tiles_readback(tile_lds[wave], w);
+    const bool valid = t < len;
+    float* out = scores + score_base[s] + (size_t)h * group * len;
+    if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, len, t))
+        return;
+    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, len, t);
+}
+
+// CCOS paged scoring, general case (pages of fewer than 64 tiles, or groups
+// past kMfmaMaxGroup): one lane per token, tiles gathered per lane. Block
+// (x, y) covers tokens [256x, 256x+256) of (sequence s, KV head h) with
+// y = s*n_kv + h; token t lives in physical page
 // page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
 __global__ __launch_bounds__(256) void score_paged_kernel(
     const uint4* __restrict__ arena, uint32_t page_shift, const uint32_t* __restrict__ page_table,
@@ -1249,25 +1303,38 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
     out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
 }
 
-// Query preparation: q_coarse = q, q_sign = sign(Z * RHT(q)).
+// Query preparation: q_coarse = q, q_sign = sign(Z * RHT(q)). One workgroup
+// per query and one lane per sign row: every lane forms RHT(q) with identical
+// arithmetic, lane s accumulates row s of Z in the reference order
+// (sequential f32 from 0.0, no contraction), and a wave ballot packs the 64
+// bits of one q_sign word.
 __global__ __launch_bounds__(256) void prepare_query_kernel(const void* __restrict__ q, int dtype,
-                                                            uint64_t n_q,
                                                             const float* __restrict__ z,
                                                             const float* __restrict__ diag,
                                                             float rht_inv, float* __restrict__ qc,
-                                                            uint4* __restrict__ qs) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_q) return;
+                                                            uint64_t* __restrict__ qs) {
+    const size_t i = blockIdx.x;
+    const uint32_t row = threadIdx.x;
+    if (row < kDC) {
+        qc[i * kDC + row] = dtype == kDtypeBF16
+                                ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(q)[i * kDC + row] << 16)
+                                : reinterpret_cast<const float*>(q)[i * kDC + row];
+    }
     float v[kDC];
     load_vec128(q, dtype, i, v);
-    float4* qo = reinterpret_cast<float4*>(qc) + i * 32;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) qo[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
     if (diag) rht128(v, diag, rht_inv);
-    uint32_t bits[8];
-    sign_bits_exact(v, z, bits);
-    qs[2 * i] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
-    qs[2 * i + 1] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
+    const float4* zr = reinterpret_cast<const float4*>(z + (size_t)row * kDC);
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kDC / 4; ++k) {
+        const float4 zz = zr[k];
+        acc += zz.x * v[4 * k];
+        acc += zz.y * v[4 * k + 1];
+        acc += zz.z * v[4 * k + 2];
+        acc += zz.w * v[4 * k + 3];
+    }
+    const uint64_t word = __ballot(acc < 0.0f);
+    if ((row & 63u) == 0) qs[i * 4 + (row >> 6)] = word;
 }
 
 // Decode: dequant_latent (tile.rs:249-255); optionally add the sign-sketch
@@ -1401,9 +1468,23 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
     const auto* base = reinterpret_cast<const unsigned long long*>(score_base);
     dim3 grid((max_len + 255) / 256, n_seq * n_kv);
     const size_t smem = group <= kMfmaMaxGroup ? staging_bytes(staging_rows(group)) : 0;
-    score_paged_kernel<<<grid, 256, smem, s>>>(static_cast<const uint4*>(arena), page_shift,
-                                            page_table, max_pages, seq_len, base, n_kv, group, qc,
-                                            reinterpret_cast<const uint32_t*>(qs), scores);
+    const uint4* ap = static_cast<const uint4*>(arena);
+    const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
+    if (page_shift >= 6 && group <= kMfmaMaxGroup) {
+#define SLHA_PAGED(R, SMEM)                                                                     \
+    score_paged_fast_kernel<R><<<grid, 256, SMEM, s>>>(ap, page_shift, page_table, max_pages,   \
+                                                       seq_len, base, n_kv, group, qc, qsw, scores)
+        if (group <= 4)
+            SLHA_PAGED(4, 0);
+        else if (group <= kRegStageMaxGroup)
+            SLHA_PAGED(16, 0);
+        else
+            SLHA_PAGED(0, smem);
+#undef SLHA_PAGED
+    } else {
+        score_paged_kernel<<<grid, 256, smem, s>>>(ap, page_shift, page_table, max_pages, seq_len,
+                                                base, n_kv, group, qc, qsw, scores);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || k == 0) return e;
     topk_rows_kernel<<<n_seq * n_kv * group, kTopkThreads, 0, s>>>(scores, seq_len, base,
@@ -1439,8 +1520,8 @@ hipError_t launch_prepare_queries(const void* q, int dtype, uint64_t n_q, const 
                                   const float* diag, float rht_inv, float* qc, uint64_t* qs,
                                   hipStream_t s) {
     if (n_q == 0) return hipSuccess;
-    prepare_query_kernel<<<(unsigned)((n_q + 255) / 256), 256, 0, s>>>(
-        q, dtype, n_q, z, diag, rht_inv, qc, reinterpret_cast<uint4*>(qs));
+    if (n_q > 0x7FFFFFFFu) return hipErrorInvalidValue;
+    prepare_query_kernel<<<(unsigned)n_q, 256, 0, s>>>(q, dtype, z, diag, rht_inv, qc, qs);
     return hipGetLastError();
 }
 

@@ -151,10 +151,9 @@ def test_score_exact_bit_identical_and_hamming(s, torch, group):
 
 @pytest.mark.parametrize("group,codec", [(4, 0), (8, 2), (20, 4), (5, None)])
 def test_score_fast_streaming_ragged(s, torch, group, codec):
-    # Enough 64-tile batches that every wave of the fast kernel streams several
-    # of them, with a ragged last batch per row (n_tok not a multiple of 64)
-    # and batches past the end of the row. codec None: random mixed-codec
-    # tiles, so waves fall back to the per-lane path inside the stream loop.
+    # Many workgroups per row, a ragged last wave per row (n_tok not a
+    # multiple of 64) and waves entirely past the end of the row. codec None:
+    # random mixed-codec tiles, so waves fall back to the per-lane path.
     n_rows, n_tok = 8, 50_001
     r = np.random.default_rng(1000 + group)
     if codec is None:
@@ -272,15 +271,19 @@ def build_paged(lens, n_kv, page_tiles, seed, tiles_src):
     return arena, table, max_pages
 
 
-@pytest.mark.parametrize("const_scores", [False, True])
-def test_paged_topk(s, torch, const_scores):
+# page_tiles >= 64 takes the wave-gather fast kernel, 16 the per-lane one;
+# flags [0] gives uniform INT4 waves (f16 MFMA path), [0, 2] mixed waves.
+@pytest.mark.parametrize("const_scores,page_tiles,flag_set,group", [
+    (False, 256, (0, 2), 4), (True, 256, (0, 2), 4), (False, 64, (0,), 4),
+    (False, 4096, (0,), 8), (False, 16, (0,), 4), (True, 64, (0,), 4)])
+def test_paged_topk(s, torch, const_scores, page_tiles, flag_set, group):
     lens = [1, 63, 64, 1000, 5000, 300]
-    n_kv, group, page_tiles, k = 2, 4, 256, 64
+    n_kv, k = 2, 64
     r = np.random.default_rng(11)
     src = {}
     for si, l in enumerate(lens):
         for h in range(n_kv):
-            t = random_tiles(l, 100 * si + h, [0, 2])
+            t = random_tiles(l, 100 * si + h, list(flag_set))
             warm = r.random(l) < 0.3
             for i in np.nonzero(warm)[0]:
                 t[i:i + 1] = o.page_out(t[i])
