@@ -124,6 +124,229 @@ def cpu_baseline(tiles_np, qc_np, qs_np, threads: int) -> dict:
     }
 
 
+def timed_steps(step, steps: int, warmup: int, stream) -> float:
+    """Mean ms per step over `steps` launches after `warmup`, HIP events on `stream`."""
+    import torch
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def timed_once(fn, stream) -> float:
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
+
+
+def line(metric, value, unit, steps, warmup, ms, dtype, config, **extra) -> dict:
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
+    out.update(extra)
+    return out
+
+
+def hbm_roofline(nbytes: float, ms: float, kernel: str) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": gbs / PEAK_HBM_GBS, "traffic": None, "kernel": kernel,
+            "algorithmic_bytes_per_launch": nbytes, "kernel_ms": ms}
+
+
+def c3_keys(torch, g, rows: int, n_tok: int, outlier_seed: int):
+    """bf16 Student-t(4) keys, [rows, n_tok, 128]; per KV head 4 fixed distinct
+    outlier channels scaled x20 (rows = seq * 8 + head)."""
+    out = torch.empty((rows, n_tok, D), dtype=torch.bfloat16, device="cuda")
+    gen = torch.Generator().manual_seed(outlier_seed)
+    chans = [torch.randperm(D, generator=gen)[:4].tolist() for _ in range(8)]
+    for r in range(rows):
+        z0 = torch.randn((n_tok, D), device="cuda", generator=g)
+        chi = torch.randn((4, n_tok, D), device="cuda", generator=g).square().mean(0)
+        t = z0 / chi.sqrt()
+        t[:, chans[r % 8]] *= 20.0
+        out[r] = t.to(torch.bfloat16)
+    return out
+
+
+def run_c3(args) -> int:
+    """16 seqs x 8 KV heads x 131072 Student-t keys, NF4 and
+    MX-INT4 (grouped INT4) run separately; 32 query heads per sequence."""
+    import torch
+
+    import slhav2_amd as s
+
+    n_seq, n_kv, n_tok = 16, 8, 131072
+    rows, n_q = n_seq * n_kv, n_seq * n_kv * GROUP
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0002)
+    keys = c3_keys(torch, g, rows, n_tok, 0x5EED0003)
+    q = torch.randn((n_q, D), device="cuda", generator=g).to(torch.bfloat16)
+    tiles = torch.empty((rows, n_tok, 128), dtype=torch.uint8, device="cuda")
+    scores = torch.empty((n_q, n_tok), dtype=torch.float32, device="cuda")
+    nbytes = rows * n_tok * TILE_BYTES + n_q * n_tok * 4 + n_q * (D * 4 + 32)
+    steps, warmup = min(args.steps, 20), min(args.warmup, 3)
+    results = {}
+    with s.Model(seed=0x5EED0004, rht=False, residual_mode=s.RESIDUAL_R) as m:
+        qc, qs = s.gpu_prepare_queries(m, q)
+        for name, codec in (("nf4", s.CODEC_NF4), ("mx_int4", s.CODEC_INT4_GROUPED)):
+            enc_ms = timed_once(lambda: s.gpu_encode(m, keys, codec, n_kv_heads=n_kv, out=tiles,
+                                                     stream=stream), stream)
+            score = s.lib.slha_gpu_score
+            vp = ctypes.c_void_p
+            a = (vp(tiles.data_ptr()), rows, n_tok, vp(qc.data_ptr()), vp(qs.data_ptr()), GROUP,
+                 s.SCORE_FAST, vp(scores.data_ptr()), None, vp(stream.cuda_stream))
+            ms = timed_steps(lambda i: score(*a), steps, warmup, stream)
+            ex = s.gpu_score(tiles[:1], qc[:GROUP], qs[:GROUP], group=GROUP, mode=s.SCORE_EXACT)
+            err = ((scores[:GROUP] - ex).abs() / (1 + ex.abs())).max().item()
+            results[name] = {"ms_per_step": ms, "tiles_per_s": n_q * n_tok / (ms * 1e-3),
+                             "roofline": hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<4u>"),
+                             "encode_keys_per_s": rows * n_tok / (enc_ms * 1e-3),
+                             "encode_ms": enc_ms, "fast_vs_exact_max_rel_err_row0": err}
+    best = results["mx_int4"]
+    print(json.dumps(line(
+        "tiles scored/s + HBM GB/s % of peak; keys encoded/s", best["tiles_per_s"], "tiles/s",
+        steps, warmup, best["ms_per_step"], "f32",
+        {"workload": "C3 batched decode, Student-t(4) keys with outliers (BASELINE configs[2])",
+         "sequences": n_seq, "kv_heads": n_kv, "tokens_per_head": n_tok, "query_heads": n_q,
+         "group": GROUP, "codecs": "nf4, mx_int4 (run separately; value = mx_int4)",
+         "parallelism": "none (1 GPU)"},
+        per_codec=results)), flush=True)
+    return 0
+
+
+def run_c4(args) -> int:
+    """1 048 576 keys, TQ3 + Hadamard RHT, per-token scale
+    log-uniform in [0.1, 10]; 64 queries scored against every tile."""
+    import torch
+
+    import slhav2_amd as s
+
+    n_keys, n_q = 1 << 20, 64
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0005)
+    u = torch.rand((n_keys, 1), device="cuda", generator=g)
+    keys = (torch.randn((n_keys, D), device="cuda", generator=g) * (0.1 * 100.0 ** u)).to(torch.bfloat16)
+    q = torch.randn((n_q, D), device="cuda", generator=g).to(torch.bfloat16)
+    tiles = torch.empty((1, n_keys, 128), dtype=torch.uint8, device="cuda")
+    scores = torch.empty((n_q, n_keys), dtype=torch.float32, device="cuda")
+    steps, warmup = min(args.steps, 20), min(args.warmup, 3)
+    with s.Model(seed=0x5EED0006, rht=True, residual_mode=s.RESIDUAL_R) as m:
+        enc_ms = timed_once(lambda: s.gpu_encode(m, keys.view(1, n_keys, D), s.CODEC_TQ3,
+                                                 out=tiles, stream=stream), stream)
+        qc, qs = s.gpu_prepare_queries(m, q)
+        score = s.lib.slha_gpu_score
+        vp = ctypes.c_void_p
+        a = (vp(tiles.data_ptr()), 1, n_keys, vp(qc.data_ptr()), vp(qs.data_ptr()), n_q,
+             s.SCORE_FAST, vp(scores.data_ptr()), None, vp(stream.cuda_stream))
+        ms = timed_steps(lambda i: score(*a), steps, warmup, stream)
+        ex = s.gpu_score(tiles[:, :4096], qc, qs, group=n_q, mode=s.SCORE_EXACT)
+        err = ((scores[:, :4096] - ex).abs() / (1 + ex.abs())).max().item()
+    nbytes = n_keys * TILE_BYTES + n_q * n_keys * 4 + n_q * (D * 4 + 32)
+    flops = n_q * n_keys * 2 * D
+    enc_bytes = n_keys * (D * 2 + TILE_BYTES)
+    print(json.dumps(line(
+        "tiles scored/s + HBM GB/s % of peak; keys encoded/s", n_q * n_keys / (ms * 1e-3),
+        "tiles/s", steps, warmup, ms, "f32",
+        {"workload": "C4 bulk encode + score, TQ3 + RHT (BASELINE configs[3])", "keys": n_keys,
+         "queries": n_q, "codec": "tq3", "rht": True, "parallelism": "none (1 GPU)"},
+        roofline=hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<0u>"),
+        score_tflops=flops / (ms * 1e-3) / 1e12, fast_vs_exact_max_rel_err_first4096=err,
+        encode={"keys_per_s": n_keys / (enc_ms * 1e-3), "ms": enc_ms,
+                "hbm_gbs": enc_bytes / (enc_ms * 1e-3) / 1e9})), flush=True)
+    return 0
+
+
+def run_c5(args) -> int:
+    """CCOS paged scoring + top-64 over 64 ragged sequences
+    in 4096-tile pages shuffled in one arena, 30 % of tiles WARM."""
+    import torch
+
+    import slhav2_amd as s
+
+    n_seq, n_kv, page, k = 64, 8, 4096, 64
+    hq = n_kv * GROUP
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator().manual_seed(0x5EED0007)
+    u = torch.rand(n_seq, generator=gen, dtype=torch.float64)
+    lens = [int(1024 * 128.0 ** float(x)) for x in u]
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0008)
+    pages = [(si, h, p) for si, L in enumerate(lens) for h in range(n_kv)
+             for p in range(-(-L // page))]
+    perm = torch.randperm(len(pages), generator=gen).tolist()
+    max_pages = max(-(-L // page) for L in lens)
+    arena = torch.zeros((len(pages) * page, 128), dtype=torch.uint8, device="cuda")
+    table = torch.zeros((n_seq, n_kv, max_pages), dtype=torch.int32)
+    valid = torch.zeros(len(pages) * page, dtype=torch.bool)
+    with s.Model(seed=0x5EED0009, rht=False, residual_mode=s.RESIDUAL_R) as m:
+        logical = {pg: i for i, pg in enumerate(pages)}
+        for si, L in enumerate(lens):
+            keys = torch.randn((n_kv, L, D), device="cuda", generator=g).to(torch.bfloat16)
+            t = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE, n_kv_heads=n_kv)
+            for h in range(n_kv):
+                for p in range(-(-L // page)):
+                    phys = perm[logical[(si, h, p)]]
+                    n = min(page, L - p * page)
+                    arena[phys * page: phys * page + n] = t[h, p * page: p * page + n]
+                    valid[phys * page: phys * page + n] = True
+                    table[si, h, p] = phys
+        slots = valid.nonzero().flatten()
+        warm = slots[torch.rand(len(slots), generator=gen) < 0.3].to(torch.int32).cuda()
+        s.gpu_ccos_apply(arena, warm, 0)
+        q = torch.randn((n_seq * hq, D), device="cuda", generator=g).to(torch.bfloat16)
+        qc, qs = s.gpu_prepare_queries(m, q)
+    seq_len = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    lens64 = torch.tensor(lens, dtype=torch.int64)
+    base = torch.zeros(n_seq, dtype=torch.int64)
+    base[1:] = torch.cumsum(lens64, 0)[:-1] * hq
+    base = base.cuda()
+    total_tiles = sum(lens) * n_kv
+    pairs = sum(lens) * hq
+    scores = torch.empty(pairs, dtype=torch.float32, device="cuda")
+    idx = torch.empty((n_seq, hq, k), dtype=torch.int32, device="cuda")
+    val = torch.empty((n_seq, hq, k), dtype=torch.float32, device="cuda")
+    table_d = table.cuda()
+    vp = ctypes.c_void_p
+    fn = s.lib.slha_gpu_score_paged_topk
+    a = (vp(arena.data_ptr()), page, vp(table_d.data_ptr()), max_pages, vp(seq_len.data_ptr()),
+         vp(base.data_ptr()), n_seq, max(lens), n_kv, GROUP, vp(qc.data_ptr()), vp(qs.data_ptr()),
+         vp(scores.data_ptr()), k, vp(idx.data_ptr()), vp(val.data_ptr()), vp(stream.cuda_stream))
+    steps, warmup = min(args.steps, 20), min(args.warmup, 3)
+    ms = timed_steps(lambda i: fn(*a), steps, warmup, stream)
+    # the score pass alone (k = 0), to split the time between the two kernels
+    a0 = a[:13] + (0,) + a[14:]
+    ms_score = timed_steps(lambda i: fn(*a0), steps, warmup, stream)
+    n_warm = int(len(warm))
+    logical_tile_bytes = (total_tiles - n_warm) * 128 + n_warm * 96
+    nbytes = (logical_tile_bytes + pairs * 4 + n_seq * hq * k * 8 + n_seq * hq * (D * 4 + 32)
+              + table.numel() * 4)
+    print(json.dumps(line(
+        "tiles scored/s + HBM GB/s % of peak (paged, top-64)", pairs / (ms * 1e-3), "tiles/s",
+        steps, warmup, ms, "f32",
+        {"workload": "C5 CCOS paged scoring + top-64 (BASELINE configs[4])", "sequences": n_seq,
+         "kv_heads": n_kv, "page_tiles": page, "tiles": total_tiles, "warm_tiles": n_warm,
+         "pairs": pairs, "max_len": max(lens), "min_len": min(lens), "k": k,
+         "parallelism": "none (1 GPU)"},
+        roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_rows_kernel"),
+        score_only_ms=ms_score, topk_ms=ms - ms_score,
+        score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9)), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +355,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c2",
+                    help="c2 (default) is the headline; c3/c4/c5 measure the other "
+                         "BASELINE configs at full size")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -141,6 +367,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.config != "c2":
+        return {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args)
 
     import torch
 

@@ -114,7 +114,9 @@ size_t slha_tile_align(void);
 const char* slha_last_error_message(void);
 void slha_clear_error(void);
 
-/* slha.h:140,147 — process-wide context; shutdown releases device buffers. */
+/* slha.h:140,147 — process-wide context. Shutdown is a no-op, as in the
+ * reference (lib.rs:331-360); device buffers the library caches live until
+ * the process ends. */
 SlhaContext* slha_init(void);
 int32_t slha_shutdown(SlhaContext* context);
 

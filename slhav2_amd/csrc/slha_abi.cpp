@@ -282,6 +282,47 @@ char* staging(size_t bytes, hipStream_t* stream) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Device workspace of the stream-ordered entry points (the paged top-k's
+// candidate lists), one grow-only buffer per (device, stream): work queued on
+// one stream never shares it with work on another. Buffers live until the
+// process ends.
+struct WorkspaceKey {
+    int device;
+    hipStream_t stream;
+    bool operator==(const WorkspaceKey& o) const { return device == o.device && stream == o.stream; }
+};
+struct WorkspaceKeyHash {
+    size_t operator()(const WorkspaceKey& k) const {
+        return std::hash<void*>()(static_cast<void*>(k.stream)) ^ (size_t)k.device * 0x9E3779B97F4A7C15ull;
+    }
+};
+struct Workspace {
+    void* buf = nullptr;
+    size_t cap = 0;
+};
+std::mutex g_workspace_mu;
+std::unordered_map<WorkspaceKey, Workspace, WorkspaceKeyHash> g_workspaces;
+
+void* stream_workspace(size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return nullptr;
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_workspace_mu);
+    Workspace& w = g_workspaces[WorkspaceKey{device, stream}];
+    if (w.cap < bytes) {
+        if (w.buf) {
+            // the old buffer may still be read by work queued on this stream
+            check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+            check_hip(hipFree(w.buf), "hipFree(workspace)");
+        }
+        w.buf = nullptr;
+        w.cap = 0;
+        check_hip(hipMalloc(&w.buf, bytes), "hipMalloc(workspace)");
+        w.cap = bytes;
+    }
+    return w.buf;
+}
+
 // GPU eq. 2.3 (exact order) over host tiles; scores written to host `out`.
 void score_host_tiles(const SciRustSlhaTile* tiles, size_t n, const float* qc, const uint64_t* qs,
                       float* out) {
@@ -754,6 +795,10 @@ int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_
         if (group == 0 || group > kMaxGroup)
             fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
         if (k > kMaxTopK) fail(SLHA_ERR_DIMENSION, "k=%zu exceeds %u", k, kMaxTopK);
+        if (k > 0 && (max_len + kTopkSeg - 1) / kTopkSeg * k > kTopkMaxCandidates)
+            fail(SLHA_ERR_DIMENSION,
+                 "top-k of rows up to max_len=%zu needs ceil(max_len/%u)*k <= %u (k=%zu)",
+                 max_len, kTopkSeg, kTopkMaxCandidates, k);
         if (n_kv_heads == 0 || n_seq * n_kv_heads > 65535 || max_len > 0xFFFFFFFFull ||
             max_pages > 0xFFFFFFFFull || (uint64_t)max_len > (uint64_t)max_pages * page_tiles)
             fail(SLHA_ERR_DIMENSION, "paged geometry out of range (n_seq=%zu n_kv=%zu max_len=%zu)",
@@ -765,12 +810,17 @@ int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_
         require_device();
         uint32_t shift = 0;
         while ((size_t(1) << shift) < page_tiles) ++shift;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        void* ws = k == 0 ? nullptr
+                          : stream_workspace(paged_topk_workspace_bytes(
+                                                 (uint32_t)n_seq, (uint32_t)max_len,
+                                                 (uint32_t)n_kv_heads, (uint32_t)group, (uint32_t)k),
+                                             s);
         check_hip(launch_score_paged_topk(arena_dev, shift, page_table_dev, (uint32_t)max_pages,
                                           seq_len_dev, score_base_dev, (uint32_t)n_seq,
                                           (uint32_t)max_len, (uint32_t)n_kv_heads, (uint32_t)group,
                                           q_coarse_dev, q_sign_dev, scores_dev, (uint32_t)k,
-                                          topk_idx_dev, topk_score_dev,
-                                          static_cast<hipStream_t>(stream)),
+                                          topk_idx_dev, topk_score_dev, ws, s),
                   "paged score kernel");
     });
 }

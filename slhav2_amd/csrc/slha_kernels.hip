@@ -818,13 +818,28 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
 // ---------------------------------------------------------------------------
 // Top-k per score row: score descending, ties to the lower token index.
 //
-// One 1024-thread workgroup per (sequence, query head) row. Scores map to
-// order-preserving u32 keys; a three-pass radix select (11 + 11 + 10 bits,
-// histograms in LDS) finds the k-th largest key T and how many keys equal to
-// T are needed; a final pass in token order collects every key > T plus the
-// lowest-index keys == T; the k winners are bitonic-sorted in LDS.
+// Two stages; each reads its input once, with coalesced branch-free loads:
+//  1. topk_segment_kernel: one 256-thread workgroup per 4096-score segment of
+//     a (sequence, query head) row, 16 scores per thread in registers; its
+//     top k go, sorted, to the row's candidate list (k slots per segment).
+//  2. topk_merge_kernel: one 1024-thread workgroup per row selects the top k
+//     of the row's candidates.
+// Both use block_topk: scores are order-preserving u32 keys; each wave sorts
+// its 64 per-thread maxima (a shuffle bitonic network) and takes the
+// r-th largest, r = ceil(kk / waves); tau = the smallest of those is a lower
+// bound of the kk-th largest key (every wave has r threads holding a key
+// >= tau), so the keys >= tau contain the whole top kk, ties included.
+// They are typically a few times kk: each one's rank in (key desc, index
+// asc) order is counted against the others and ranks < kk are written in
+// that order. When they do not fit in LDS (heavy ties), an exact 8-bit radix
+// select finds the kk-th largest key T and the winners are the keys > T
+// plus the first keys == T in item order (item order is index order among
+// equal keys in both stages).
 
-constexpr int kTopkThreads = 1024;
+constexpr int kSegThreads = 256;       // 16 scores per thread (kTopkSeg = 4096)
+constexpr int kTopkThreads = 1024;     // merge workgroup
+constexpr int kMergePer = (int)(kTopkMaxCandidates / kTopkThreads);  // candidates per merge thread
+constexpr uint32_t kTopkCap = 1024;    // candidates ranked in LDS
 
 __device__ __forceinline__ uint32_t order_key(float f) {
     // -0.0 and +0.0 compare equal, so they share a key (ties then go by index).
@@ -835,157 +850,262 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// Finds the digit bin holding the need-th largest element (1-based) from the
-// top of hist[nbins]; returns the bin and the count strictly above it.
-__device__ __forceinline__ void select_bin(uint32_t* hist, int nbins, uint32_t need,
-                                          uint32_t* sh_bin, uint32_t* sh_above) {
-    // Suffix sums: hist[i] <- sum_{j >= i} hist[j] (Hillis-Steele over LDS).
-    for (int off = 1; off < nbins; off <<= 1) {
-        uint32_t v[2] = {0, 0};
-        for (int r = 0; r < 2; ++r) {
-            const int i = threadIdx.x + r * kTopkThreads;
-            if (i < nbins) v[r] = hist[i] + ((i + off < nbins) ? hist[i + off] : 0u);
-        }
-        __syncthreads();
-        for (int r = 0; r < 2; ++r) {
-            const int i = threadIdx.x + r * kTopkThreads;
-            if (i < nbins) hist[i] = v[r];
-        }
-        __syncthreads();
+// Exclusive prefix sum of one u32 per thread over a workgroup of NT threads
+// (NT a multiple of 64); `tmp` holds NT/64 words of LDS. Returns the
+// exclusive prefix; *total receives the sum. Contains barriers.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* tmp,
+                                                         uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    uint32_t incl = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off);
+        if (lane >= (uint32_t)off) incl += y;
     }
-    for (int r = 0; r < 2; ++r) {
-        const int i = threadIdx.x + r * kTopkThreads;
-        if (i < nbins) {
-            const uint32_t ge = hist[i];
-            const uint32_t gt = (i + 1 < nbins) ? hist[i + 1] : 0u;
-            if (ge >= need && gt < need) {
-                *sh_bin = (uint32_t)i;
-                *sh_above = gt;
-            }
-        }
+    if (lane == 63) tmp[wv] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        const uint32_t t = tmp[w];
+        before += (uint32_t)w < wv ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - x;
+}
+
+// Max of one u32 per lane across the wave (DPP row steps, then row
+// broadcasts 15 and 31 leave it in lane 63).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+#define SLHA_DPP_UMAX(ctrl, rows) \
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rows, 0xF, false))
+    SLHA_DPP_UMAX(0xB1, 0xF);   // quad_perm [1,0,3,2]
+    SLHA_DPP_UMAX(0x4E, 0xF);   // quad_perm [2,3,0,1]
+    SLHA_DPP_UMAX(0x141, 0xF);  // row_half_mirror
+    SLHA_DPP_UMAX(0x140, 0xF);  // row_mirror
+    SLHA_DPP_UMAX(0x142, 0xA);  // row_bcast:15
+    SLHA_DPP_UMAX(0x143, 0xC);  // row_bcast:31
+#undef SLHA_DPP_UMAX
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// r-th largest (1-based, 1 <= r <= 64) of one u32 per lane across the wave:
+// r rounds of "take the maximum, retire the lowest lane holding it".
+__device__ __forceinline__ uint32_t wave_rth_largest(uint32_t x, uint32_t r) {
+    const uint32_t lane = threadIdx.x & 63u;
+    bool live = true;
+    uint32_t m = 0;
+    for (uint32_t i = 0; i < r; ++i) {
+        m = wave_max_u32(live ? x : 0u);
+        const unsigned long long holders = __ballot(live && x == m);
+        if (holders == 0ull) break;  // fewer than r live lanes: m is 0 already
+        if (lane == (uint32_t)__ffsll((long long)holders) - 1u) live = false;
+    }
+    return m;
+}
+
+// hist[256]: counts of the current 8-bit digit; finds the bin holding the
+// need-th largest key and the count of keys above it (threads 0..255 own one
+// bin each). Contains barriers.
+template <int NT>
+__device__ __forceinline__ void select_digit(const uint32_t* hist, uint32_t need, uint32_t* tmp,
+                                             uint32_t* sh_bin, uint32_t* sh_above) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t cnt = t < 256u ? hist[255u - t] : 0u;  // thread t <-> bin 255 - t
+    uint32_t total;
+    const uint32_t above = block_exclusive_scan<NT>(cnt, tmp, &total);
+    if (t < 256u && above < need && above + cnt >= need) {
+        *sh_bin = 255u - t;
+        *sh_above = above;
     }
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
-    const float* __restrict__ scores, const uint32_t* __restrict__ seq_len,
-    const unsigned long long* __restrict__ score_base, uint32_t hq, uint32_t k,
-    uint32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
-    __shared__ uint32_t hist[2048];
-    __shared__ uint32_t sel_key[kMaxTopK];
-    __shared__ uint32_t sel_idx[kMaxTopK];
-    __shared__ uint32_t sh_bin, sh_above, sh_count, sh_eq_taken;
-    __shared__ uint32_t wave_eq[kTopkThreads / 64];
-    const uint32_t row = blockIdx.x;
-    const uint32_t s = row / hq, qh = row - s * hq;
-    const uint32_t len = seq_len[s];
-    const float* sc = scores + score_base[s] + (size_t)qh * len;
-    const uint32_t kk = k < len ? k : len;
-
-    uint32_t prefix = 0, prefix_mask = 0, need = kk;
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    for (int pass = 0; pass < 3 && kk > 0; ++pass) {
-        const int nb = 1 << widths[pass];
-        for (int i = threadIdx.x; i < 2048; i += kTopkThreads) hist[i] = 0u;
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < len; i += kTopkThreads) {
-            const uint32_t key = order_key(sc[i]);
-            if ((key & prefix_mask) == prefix)
-                atomicAdd(&hist[(key >> shifts[pass]) & (uint32_t)(nb - 1)], 1u);
-        }
-        __syncthreads();
-        select_bin(hist, nb, need, &sh_bin, &sh_above);
-        need -= sh_above;
-        prefix |= sh_bin << shifts[pass];
-        prefix_mask |= (uint32_t)(nb - 1) << shifts[pass];
-    }
-    const uint32_t thr = prefix;  // exact k-th largest key; `need` keys == thr are taken
-
-    if (threadIdx.x == 0) {
-        sh_count = 0;
-        sh_eq_taken = 0;
-    }
+// Top kk (<= kMaxTopK, <= number of valid items) of the workgroup's items:
+// thread t holds items j*NT + t (j < PER) with key[j], idx[j], valid if
+// ok[j]. Writes the winners, ranked, to out_key/out_idx[0..kk). Shared-memory
+// scratch comes from the caller. Every thread calls it.
+template <int NT, int PER>
+__device__ __forceinline__ void block_topk(const uint32_t (&key)[PER], const uint32_t (&idx)[PER],
+                                           const bool (&ok)[PER], uint32_t kk, uint2* cand,
+                                           uint32_t* rank, uint32_t* hist, uint32_t* tmp,
+                                           uint32_t* sh,
+                                           uint32_t* __restrict__ out_key,
+                                           uint32_t* __restrict__ out_idx) {
+    constexpr uint32_t kWaves = NT / 64;
+    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) m = ok[j] ? max(m, key[j]) : m;
+    uint32_t r = (kk + kWaves - 1) / kWaves;
+    r = r < 1u ? 1u : (r > 64u ? 64u : r);
+    const uint32_t tau_w = wave_rth_largest(m, r);
+    if (lane == 0) tmp[wv] = tau_w;
     __syncthreads();
-    // Collect in token order: chunks of kTopkThreads, ranks of == thr by
-    // ballot prefix so the lowest indices win the ties.
-    for (uint32_t base = 0; base < len && kk > 0; base += kTopkThreads) {
-        const uint32_t i = base + threadIdx.x;
-        uint32_t key = 0;
-        bool gt = false, eq = false;
-        if (i < len) {
-            key = order_key(sc[i]);
-            gt = key > thr;
-            eq = key == thr;
-        }
-        if (gt) {
-            const uint32_t slot = atomicAdd(&sh_count, 1u);
-            if (slot < kMaxTopK) {
-                sel_key[slot] = key;
-                sel_idx[slot] = i;
-            }
-        }
-        const unsigned long long bal = __ballot(eq);
-        const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-        if (lane == 0) wave_eq[wv] = (uint32_t)__popcll(bal);
-        __syncthreads();
-        uint32_t before = 0;
-        for (uint32_t j = 0; j < wv; ++j) before += wave_eq[j];
-        const uint32_t rank = sh_eq_taken + before +
-                              (uint32_t)__popcll(bal & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-        if (eq && rank < need) {
-            const uint32_t slot = atomicAdd(&sh_count, 1u);
-            if (slot < kMaxTopK) {
-                sel_key[slot] = key;
-                sel_idx[slot] = i;
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t tot = 0;
-            for (uint32_t j = 0; j < kTopkThreads / 64; ++j) tot += wave_eq[j];
-            sh_eq_taken += tot;
-        }
-        __syncthreads();
-    }
-    // Pad to kMaxTopK and bitonic-sort by (key desc, idx asc).
-    for (uint32_t i = threadIdx.x; i < kMaxTopK; i += kTopkThreads) {
-        if (i >= kk) {
-            sel_key[i] = 0u;
-            sel_idx[i] = 0xFFFFFFFFu;
-        }
-    }
+    uint32_t tau = 0xFFFFFFFFu;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) tau = min(tau, tmp[w]);
     __syncthreads();
-    for (uint32_t size = 2; size <= kMaxTopK; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = threadIdx.x; i < kMaxTopK; i += kTopkThreads) {
-                const uint32_t j = i ^ stride;
-                if (j > i) {
-                    // "a before b" iff a.key > b.key or (equal and a.idx < b.idx)
-                    const uint32_t ka = sel_key[i], kb = sel_key[j];
-                    const uint32_t ia = sel_idx[i], ib = sel_idx[j];
-                    const bool a_first = ka > kb || (ka == kb && ia < ib);
-                    const bool up = (i & size) == 0;
-                    if (up != a_first) {
-                        sel_key[i] = kb;
-                        sel_key[j] = ka;
-                        sel_idx[i] = ib;
-                        sel_idx[j] = ia;
-                    }
-                }
-            }
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) c += (ok[j] && key[j] >= tau) ? 1u : 0u;
+    uint32_t total;
+    uint32_t pos = block_exclusive_scan<NT>(c, tmp, &total);
+    if (total <= kTopkCap) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (ok[j] && key[j] >= tau) cand[pos++] = make_uint2(key[j], idx[j]);
+    } else {
+        // exact radix select over the valid keys
+        uint32_t prefix = 0, mask = 0, need = kk;
+#pragma unroll 1
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (uint32_t i = threadIdx.x; i < 256u; i += NT) hist[i] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+                if (ok[j] && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+            __syncthreads();
+            select_digit<NT>(hist, need, tmp, &sh[0], &sh[1]);
+            need -= sh[1];
+            prefix |= sh[0] << shift;
+            mask |= 255u << shift;
             __syncthreads();
         }
-    }
-    for (uint32_t i = threadIdx.x; i < k; i += kTopkThreads) {
-        const size_t o = (size_t)row * k + i;
-        if (i < kk) {
-            topk_idx[o] = sel_idx[i];
-            topk_val[o] = key_to_float(sel_key[i]);
-        } else {
-            topk_idx[o] = 0xFFFFFFFFu;
-            topk_val[o] = -INFINITY;
+        const uint32_t thr = prefix;
+        // winners: keys > thr, then the first `need` keys == thr in item order
+        total = 0;
+#pragma unroll 1
+        for (int j = 0; j < PER; ++j) {
+            const bool eq = ok[j] && key[j] == thr;
+            uint32_t n_eq;
+            const uint32_t rk = block_exclusive_scan<NT>(eq ? 1u : 0u, tmp, &n_eq);
+            const bool win = (ok[j] && key[j] > thr) || (eq && rk < need);
+            uint32_t n_win;
+            const uint32_t p = block_exclusive_scan<NT>(win ? 1u : 0u, tmp, &n_win);
+            if (win) cand[total + p] = make_uint2(key[j], idx[j]);
+            total += n_win;
+            need = need > n_eq ? need - n_eq : 0u;
         }
+    }
+    // rank by (key desc, index asc); ranks < kk are the result, in order.
+    // Candidate i's rank is summed over `slices` threads, each comparing it
+    // with a contiguous slice of the others.
+    for (uint32_t i = threadIdx.x; i < total; i += NT) rank[i] = 0u;
+    __syncthreads();
+    const uint32_t slices = total ? (NT / total > 0 ? NT / total : 1u) : 1u;
+    const uint32_t per = (total + slices - 1) / slices;
+    for (uint32_t p = threadIdx.x; p < total * slices; p += NT) {
+        const uint32_t i = p / slices, q = p - i * slices;
+        const uint2 me = cand[i];
+        const uint32_t j0 = q * per, j1 = j0 + per < total ? j0 + per : total;
+        uint32_t r = 0;
+        uint32_t j = j0;
+        for (; j + 4 <= j1; j += 4) {
+            const uint2 o0 = cand[j], o1 = cand[j + 1], o2 = cand[j + 2], o3 = cand[j + 3];
+            r += (o0.x > me.x || (o0.x == me.x && o0.y < me.y)) ? 1u : 0u;
+            r += (o1.x > me.x || (o1.x == me.x && o1.y < me.y)) ? 1u : 0u;
+            r += (o2.x > me.x || (o2.x == me.x && o2.y < me.y)) ? 1u : 0u;
+            r += (o3.x > me.x || (o3.x == me.x && o3.y < me.y)) ? 1u : 0u;
+        }
+        for (; j < j1; ++j) {
+            const uint2 o = cand[j];
+            r += (o.x > me.x || (o.x == me.x && o.y < me.y)) ? 1u : 0u;
+        }
+        if (r) atomicAdd(&rank[i], r);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < total; i += NT) {
+        const uint32_t rk = rank[i];
+        if (rk < kk) {
+            out_key[rk] = cand[i].x;
+            out_idx[rk] = cand[i].y;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSegThreads) void topk_segment_kernel(
+    const float* __restrict__ scores, const uint32_t* __restrict__ seq_len,
+    const unsigned long long* __restrict__ score_base, uint32_t hq, uint32_t k, uint32_t nseg_max,
+    uint32_t* __restrict__ cand_key, uint32_t* __restrict__ cand_idx) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t tmp[kSegThreads / 64];
+    __shared__ uint32_t sh[2];
+    __shared__ uint2 cand[kTopkCap];
+    __shared__ uint32_t rank[kTopkCap];
+    const uint32_t row = blockIdx.y;
+    const uint32_t s = row / hq, qh = row - s * hq;
+    const uint32_t len = seq_len[s];
+    const unsigned long long sbase = score_base[s];  // issued with seq_len
+    const uint32_t start = blockIdx.x * kTopkSeg;
+    if (start >= len) return;  // whole segment past this sequence
+    const uint32_t n = len - start < kTopkSeg ? len - start : kTopkSeg;
+    const uint32_t kk = k < n ? k : n;
+    constexpr int PER = kTopkSeg / kSegThreads;
+    // Item j of thread t is score start + j*256 + t; the buffer range ends at
+    // the segment's last score, so the loads past it read zero without a
+    // branch and all 16 are in flight together.
+    const float* sc = scores + sbase + (size_t)qh * len + start;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(sc), 0, __builtin_amdgcn_readfirstlane(n * 4u), 0x00020000);
+    uint32_t key[PER], idx[PER];
+    bool ok[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const uint32_t e = j * kSegThreads + threadIdx.x;
+        key[j] = order_key(__builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, e * 4u, 0, 0)));
+        idx[j] = start + e;
+        ok[j] = e < n;
+    }
+    const size_t o = ((size_t)row * nseg_max + blockIdx.x) * k;
+    block_topk<kSegThreads, PER>(key, idx, ok, kk, cand, rank, hist, tmp, sh, cand_key + o,
+                                 cand_idx + o);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(
+    const uint32_t* __restrict__ cand_key, const uint32_t* __restrict__ cand_idx,
+    const uint32_t* __restrict__ seq_len, uint32_t hq, uint32_t k, uint32_t nseg_max,
+    uint32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t tmp[kTopkThreads / 64];
+    __shared__ uint32_t sh[2];
+    __shared__ uint2 cand[kTopkCap];
+    __shared__ uint32_t rank[kTopkCap];
+    __shared__ uint32_t sel_key[kMaxTopK];
+    __shared__ uint32_t sel_idx[kMaxTopK];
+    const uint32_t row = blockIdx.x;
+    const uint32_t s = row / hq;
+    const uint32_t len = seq_len[s];
+    const uint32_t kk = k < len ? k : len;
+    const uint32_t nseg = (len + kTopkSeg - 1) / kTopkSeg;
+    const size_t base = (size_t)row * nseg_max * k;
+    // Segment g holds min(k, len - g*kTopkSeg) candidates and every segment
+    // but the last is full, so the valid candidates are [0, m_valid), at most
+    // kTopkMaxCandidates = kTopkThreads * kMergePer.
+    const uint32_t rem_last = nseg ? len - (nseg - 1) * kTopkSeg : 0u;
+    const uint32_t m_valid = nseg ? (nseg - 1) * k + (rem_last < k ? rem_last : k) : 0u;
+    if (kk > 0) {
+        uint32_t key[kMergePer], idx[kMergePer];
+        bool ok[kMergePer];
+#pragma unroll
+        for (int j = 0; j < kMergePer; ++j) {
+            const uint32_t c = j * kTopkThreads + threadIdx.x;
+            ok[j] = c < m_valid;
+            key[j] = ok[j] ? cand_key[base + c] : 0u;
+            idx[j] = ok[j] ? cand_idx[base + c] : 0u;
+        }
+        block_topk<kTopkThreads, kMergePer>(key, idx, ok, kk, cand, rank, hist, tmp, sh,
+                                            sel_key, sel_idx);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < k; i += kTopkThreads) {
+        const size_t oo = (size_t)row * k + i;
+        topk_idx[oo] = i < kk ? sel_idx[i] : 0xFFFFFFFFu;
+        topk_val[oo] = i < kk ? key_to_float(sel_key[i]) : -INFINITY;
     }
 }
 
@@ -1463,7 +1583,8 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
                                   const uint32_t* seq_len, const uint64_t* score_base,
                                   uint32_t n_seq, uint32_t max_len, uint32_t n_kv, uint32_t group,
                                   const float* qc, const uint64_t* qs, float* scores, uint32_t k,
-                                  uint32_t* topk_idx, float* topk_val, hipStream_t s) {
+                                  uint32_t* topk_idx, float* topk_val, void* workspace,
+                                  hipStream_t s) {
     if (n_seq == 0 || max_len == 0) return hipSuccess;
     const auto* base = reinterpret_cast<const unsigned long long*>(score_base);
     dim3 grid((max_len + 255) / 256, n_seq * n_kv);
@@ -1487,10 +1608,25 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || k == 0) return e;
-    topk_rows_kernel<<<n_seq * n_kv * group, kTopkThreads, 0, s>>>(scores, seq_len, base,
-                                                                    n_kv * group, k, topk_idx,
-                                                                    topk_val);
+    const uint32_t hq = n_kv * group, rows = n_seq * hq;
+    const uint32_t nseg = (max_len + kTopkSeg - 1) / kTopkSeg;
+    if ((uint64_t)nseg * k > kTopkMaxCandidates) return hipErrorInvalidValue;  // checked by the ABI
+    uint32_t* cand_key = static_cast<uint32_t*>(workspace);
+    uint32_t* cand_idx = cand_key + (size_t)rows * nseg * k;
+    topk_segment_kernel<<<dim3(nseg, rows), kSegThreads, 0, s>>>(scores, seq_len, base, hq, k, nseg,
+                                                                 cand_key, cand_idx);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    topk_merge_kernel<<<rows, kTopkThreads, 0, s>>>(cand_key, cand_idx, seq_len, hq, k, nseg,
+                                                    topk_idx, topk_val);
     return hipGetLastError();
+}
+
+size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
+                                  uint32_t group, uint32_t k) {
+    const size_t rows = (size_t)n_seq * n_kv * group;
+    const size_t nseg = (max_len + kTopkSeg - 1) / kTopkSeg;
+    return rows * nseg * k * 2 * sizeof(uint32_t);
 }
 
 hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,

@@ -14,8 +14,12 @@ constexpr int kDtypeF32 = 0, kDtypeBF16 = 1;
 constexpr int kResidualZ = 0, kResidualR = 1;
 // Largest query group one scoring launch serves (LDS holds group*8 sums).
 constexpr uint32_t kMaxGroup = 256;
-// Largest k of the paged top-k (a power of two: the winners are bitonic-sorted).
+// Largest k of the paged top-k.
 constexpr uint32_t kMaxTopK = 256;
+// The paged top-k selects per 4096-score segment, then merges at most
+// kTopkMaxCandidates segment winners per row: ceil(max_len/4096) * k <= 8192.
+constexpr uint32_t kTopkSeg = 4096;
+constexpr uint32_t kTopkMaxCandidates = 8192;
 
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
@@ -25,7 +29,11 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
                                   const uint32_t* seq_len, const uint64_t* score_base,
                                   uint32_t n_seq, uint32_t max_len, uint32_t n_kv, uint32_t group,
                                   const float* qc, const uint64_t* qs, float* scores, uint32_t k,
-                                  uint32_t* topk_idx, float* topk_val, hipStream_t s);
+                                  uint32_t* topk_idx, float* topk_val, void* workspace,
+                                  hipStream_t s);
+// Device bytes of the `workspace` launch_score_paged_topk needs (top-k candidates).
+size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
+                                  uint32_t group, uint32_t k);
 hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
                          uint32_t n_kv, uint32_t pos0, int codec, int residual_mode, int warm,
                          const float* z, const float* diag, float lambda_c, float rht_inv,
