@@ -111,11 +111,11 @@ int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev
  * token index) go to topk_idx_dev / topk_score_dev[(s*n_kv_heads*group + qh)*k + i];
  * entries past len(s) are 0xFFFFFFFF / -inf. WARM tiles score coarse-only
  * (ccos.rs:320-355 via FLAG_WARM). 1 <= k <= 256 with
- * ceil(max_len / 4096) * k <= 8192 (k = 64: rows up to 524 288 tokens), or
- * k = 0 to skip top-k. The top-k stage keeps its candidate lists in a device
- * workspace the library allocates per (device, stream) on first use and
- * grows as needed: n_seq * n_kv_heads * group * ceil(max_len / 4096) * k * 8
- * bytes.
+ * ceil(max_len / 16384) * k <= 8192 (k = 64: rows up to 2 097 152 tokens),
+ * or k = 0 to skip top-k. The top-k stage keeps its candidate lists in a
+ * device workspace the library allocates per (device, stream) on first use
+ * and grows as needed: n_seq * n_kv_heads * group * ceil(max_len / 16384) *
+ * k * 8 bytes.
  */
 int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_tiles,
                                   const uint32_t* page_table_dev, size_t max_pages,

@@ -819,8 +819,8 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
 // Top-k per score row: score descending, ties to the lower token index.
 //
 // Two stages; each reads its input once, with coalesced branch-free loads:
-//  1. topk_segment_kernel: one 256-thread workgroup per 4096-score segment of
-//     a (sequence, query head) row, 16 scores per thread in registers; its
+//  1. topk_segment_kernel: one 256-thread workgroup per 16384-score segment
+//     of a (sequence, query head) row, 64 scores per thread in registers; its
 //     top k go, sorted, to the row's candidate list (k slots per segment).
 //  2. topk_merge_kernel: one 1024-thread workgroup per row selects the top k
 //     of the row's candidates.
@@ -836,7 +836,7 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
 // plus the first keys == T in item order (item order is index order among
 // equal keys in both stages).
 
-constexpr int kSegThreads = 256;       // 16 scores per thread (kTopkSeg = 4096)
+constexpr int kSegThreads = 256;       // 64 scores per thread (kTopkSeg = 16384)
 constexpr int kTopkThreads = 1024;     // merge workgroup
 constexpr int kMergePer = (int)(kTopkMaxCandidates / kTopkThreads);  // candidates per merge thread
 constexpr uint32_t kTopkCap = 1024;    // candidates ranked in LDS
@@ -924,22 +924,50 @@ __device__ __forceinline__ void select_digit(const uint32_t* hist, uint32_t need
     __syncthreads();
 }
 
+// Exact radix select over the valid items of the workgroup: the need-th
+// largest of value(j) among items with take(j) (8-bit digits, LDS
+// histograms). Returns it and sets *need_eq to how many items equal to it
+// are among the top `need`. Every thread calls it.
+template <int NT, int PER, typename Val, typename Take>
+__device__ __forceinline__ uint32_t radix_select(Val value, Take take, uint32_t need,
+                                                 uint32_t* hist, uint32_t* tmp, uint32_t* sh,
+                                                 uint32_t* need_eq) {
+    uint32_t prefix = 0, mask = 0;
+#pragma unroll 1
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (uint32_t i = threadIdx.x; i < 256u; i += NT) hist[i] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const uint32_t v = value(j);
+            if (take(j) && (v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        select_digit<NT>(hist, need, tmp, &sh[0], &sh[1]);
+        need -= sh[1];
+        prefix |= sh[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    *need_eq = need;
+    return prefix;
+}
+
 // Top kk (<= kMaxTopK, <= number of valid items) of the workgroup's items:
-// thread t holds items j*NT + t (j < PER) with key[j], idx[j], valid if
-// ok[j]. Writes the winners, ranked, to out_key/out_idx[0..kk). Shared-memory
-// scratch comes from the caller. Every thread calls it.
-template <int NT, int PER>
-__device__ __forceinline__ void block_topk(const uint32_t (&key)[PER], const uint32_t (&idx)[PER],
-                                           const bool (&ok)[PER], uint32_t kk, uint2* cand,
-                                           uint32_t* rank, uint32_t* hist, uint32_t* tmp,
-                                           uint32_t* sh,
+// thread t holds items j = 0..PER-1 with key_at(j), index idx_at(j) (unique)
+// and ok_at(j) (valid). Writes the winners, ranked, to out_key/out_idx[0..kk).
+// Shared-memory scratch comes from the caller. Every thread calls it.
+template <int NT, int PER, typename KeyAt, typename IdxAt, typename OkAt>
+__device__ __forceinline__ void block_topk(KeyAt key_at, IdxAt idx_at, OkAt ok_at, uint32_t kk,
+                                           uint2* cand, uint32_t* rank, uint32_t* hist,
+                                           uint32_t* tmp, uint32_t* sh,
                                            uint32_t* __restrict__ out_key,
                                            uint32_t* __restrict__ out_idx) {
     constexpr uint32_t kWaves = NT / 64;
     const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     uint32_t m = 0;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) m = ok[j] ? max(m, key[j]) : m;
+    for (int j = 0; j < PER; ++j) m = ok_at(j) ? max(m, key_at(j)) : m;
     uint32_t r = (kk + kWaves - 1) / kWaves;
     r = r < 1u ? 1u : (r > 64u ? 64u : r);
     const uint32_t tau_w = wave_rth_largest(m, r);
@@ -951,45 +979,33 @@ __device__ __forceinline__ void block_topk(const uint32_t (&key)[PER], const uin
     __syncthreads();
     uint32_t c = 0;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) c += (ok[j] && key[j] >= tau) ? 1u : 0u;
+    for (int j = 0; j < PER; ++j) c += (ok_at(j) && key_at(j) >= tau) ? 1u : 0u;
     uint32_t total;
     uint32_t pos = block_exclusive_scan<NT>(c, tmp, &total);
     if (total <= kTopkCap) {
 #pragma unroll
         for (int j = 0; j < PER; ++j)
-            if (ok[j] && key[j] >= tau) cand[pos++] = make_uint2(key[j], idx[j]);
+            if (ok_at(j) && key_at(j) >= tau) cand[pos++] = make_uint2(key_at(j), idx_at(j));
     } else {
-        // exact radix select over the valid keys
-        uint32_t prefix = 0, mask = 0, need = kk;
-#pragma unroll 1
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (uint32_t i = threadIdx.x; i < 256u; i += NT) hist[i] = 0u;
-            __syncthreads();
+        // Heavy ties: the kk-th largest key T, then among the keys == T the
+        // `need` lowest indices (the largest ~index), both by radix select.
+        uint32_t need;
+        const uint32_t thr = radix_select<NT, PER>(key_at, ok_at, kk, hist, tmp, sh, &need);
+        auto is_eq = [&](int j) { return ok_at(j) && key_at(j) == thr; };
+        auto inv_idx = [&](int j) { return ~idx_at(j); };
+        uint32_t one;
+        const uint32_t ithr = need ? radix_select<NT, PER>(inv_idx, is_eq, need, hist, tmp, sh, &one)
+                                   : 0xFFFFFFFFu;
+        auto win = [&](int j) {
+            return ok_at(j) && (key_at(j) > thr || (need && key_at(j) == thr && ~idx_at(j) >= ithr));
+        };
+        c = 0;
 #pragma unroll
-            for (int j = 0; j < PER; ++j)
-                if (ok[j] && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
-            __syncthreads();
-            select_digit<NT>(hist, need, tmp, &sh[0], &sh[1]);
-            need -= sh[1];
-            prefix |= sh[0] << shift;
-            mask |= 255u << shift;
-            __syncthreads();
-        }
-        const uint32_t thr = prefix;
-        // winners: keys > thr, then the first `need` keys == thr in item order
-        total = 0;
-#pragma unroll 1
-        for (int j = 0; j < PER; ++j) {
-            const bool eq = ok[j] && key[j] == thr;
-            uint32_t n_eq;
-            const uint32_t rk = block_exclusive_scan<NT>(eq ? 1u : 0u, tmp, &n_eq);
-            const bool win = (ok[j] && key[j] > thr) || (eq && rk < need);
-            uint32_t n_win;
-            const uint32_t p = block_exclusive_scan<NT>(win ? 1u : 0u, tmp, &n_win);
-            if (win) cand[total + p] = make_uint2(key[j], idx[j]);
-            total += n_win;
-            need = need > n_eq ? need - n_eq : 0u;
-        }
+        for (int j = 0; j < PER; ++j) c += win(j) ? 1u : 0u;
+        pos = block_exclusive_scan<NT>(c, tmp, &total);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (win(j)) cand[pos++] = make_uint2(key_at(j), idx_at(j));
     }
     // rank by (key desc, index asc); ranks < kk are the result, in order.
     // Candidate i's rank is summed over `slices` threads, each comparing it
@@ -1002,20 +1018,20 @@ __device__ __forceinline__ void block_topk(const uint32_t (&key)[PER], const uin
         const uint32_t i = p / slices, q = p - i * slices;
         const uint2 me = cand[i];
         const uint32_t j0 = q * per, j1 = j0 + per < total ? j0 + per : total;
-        uint32_t r = 0;
+        uint32_t rk = 0;
         uint32_t j = j0;
         for (; j + 4 <= j1; j += 4) {
             const uint2 o0 = cand[j], o1 = cand[j + 1], o2 = cand[j + 2], o3 = cand[j + 3];
-            r += (o0.x > me.x || (o0.x == me.x && o0.y < me.y)) ? 1u : 0u;
-            r += (o1.x > me.x || (o1.x == me.x && o1.y < me.y)) ? 1u : 0u;
-            r += (o2.x > me.x || (o2.x == me.x && o2.y < me.y)) ? 1u : 0u;
-            r += (o3.x > me.x || (o3.x == me.x && o3.y < me.y)) ? 1u : 0u;
+            rk += (o0.x > me.x || (o0.x == me.x && o0.y < me.y)) ? 1u : 0u;
+            rk += (o1.x > me.x || (o1.x == me.x && o1.y < me.y)) ? 1u : 0u;
+            rk += (o2.x > me.x || (o2.x == me.x && o2.y < me.y)) ? 1u : 0u;
+            rk += (o3.x > me.x || (o3.x == me.x && o3.y < me.y)) ? 1u : 0u;
         }
         for (; j < j1; ++j) {
             const uint2 o = cand[j];
-            r += (o.x > me.x || (o.x == me.x && o.y < me.y)) ? 1u : 0u;
+            rk += (o.x > me.x || (o.x == me.x && o.y < me.y)) ? 1u : 0u;
         }
-        if (r) atomicAdd(&rank[i], r);
+        if (rk) atomicAdd(&rank[i], rk);
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < total; i += NT) {
@@ -1047,23 +1063,21 @@ __global__ __launch_bounds__(kSegThreads) void topk_segment_kernel(
     constexpr int PER = kTopkSeg / kSegThreads;
     // Item j of thread t is score start + j*256 + t; the buffer range ends at
     // the segment's last score, so the loads past it read zero without a
-    // branch and all 16 are in flight together.
+    // branch and all 64 are in flight together.
     const float* sc = scores + sbase + (size_t)qh * len + start;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(sc), 0, __builtin_amdgcn_readfirstlane(n * 4u), 0x00020000);
-    uint32_t key[PER], idx[PER];
-    bool ok[PER];
+    uint32_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const uint32_t e = j * kSegThreads + threadIdx.x;
+    for (int j = 0; j < PER; ++j)
         key[j] = order_key(__builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, e * 4u, 0, 0)));
-        idx[j] = start + e;
-        ok[j] = e < n;
-    }
+            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (j * kSegThreads + threadIdx.x) * 4u, 0, 0)));
     const size_t o = ((size_t)row * nseg_max + blockIdx.x) * k;
-    block_topk<kSegThreads, PER>(key, idx, ok, kk, cand, rank, hist, tmp, sh, cand_key + o,
-                                 cand_idx + o);
+    block_topk<kSegThreads, PER>(
+        [&](int j) { return key[j]; },
+        [&](int j) { return start + (uint32_t)j * kSegThreads + threadIdx.x; },
+        [&](int j) { return (uint32_t)j * kSegThreads + threadIdx.x < n; }, kk, cand, rank, hist,
+        tmp, sh, cand_key + o, cand_idx + o);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(
@@ -1098,8 +1112,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(
             key[j] = ok[j] ? cand_key[base + c] : 0u;
             idx[j] = ok[j] ? cand_idx[base + c] : 0u;
         }
-        block_topk<kTopkThreads, kMergePer>(key, idx, ok, kk, cand, rank, hist, tmp, sh,
-                                            sel_key, sel_idx);
+        block_topk<kTopkThreads, kMergePer>(
+            [&](int j) { return key[j]; }, [&](int j) { return idx[j]; },
+            [&](int j) { return ok[j]; }, kk, cand, rank, hist, tmp, sh, sel_key, sel_idx);
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < k; i += kTopkThreads) {

@@ -16,9 +16,9 @@ constexpr int kResidualZ = 0, kResidualR = 1;
 constexpr uint32_t kMaxGroup = 256;
 // Largest k of the paged top-k.
 constexpr uint32_t kMaxTopK = 256;
-// The paged top-k selects per 4096-score segment, then merges at most
-// kTopkMaxCandidates segment winners per row: ceil(max_len/4096) * k <= 8192.
-constexpr uint32_t kTopkSeg = 4096;
+// The paged top-k selects per 16384-score segment, then merges at most
+// kTopkMaxCandidates segment winners per row: ceil(max_len/16384) * k <= 8192.
+constexpr uint32_t kTopkSeg = 16384;
 constexpr uint32_t kTopkMaxCandidates = 8192;
 
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
