@@ -719,6 +719,228 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
+// Wide-group scoring (group > 16, e.g. 64 queries per tile) on
+// v_mfma_f32_16x16x32_f16: rows = queries (blocks of 16), columns = tiles
+// (blocks of 16), K = 32 dims per instruction. Lane L supplies A row / B
+// column L % 16 for the 8 consecutive K slots 8 (L / 16) .. +7, and holds
+// C[4 (L / 16) + r][L % 16]. K is permuted so that lane group h = L / 16
+// covers latent dword 4h + ks at K-step ks (dims 8 (4h + ks) .. +7), in the
+// (d0, d4, d1, d5 | d2, d6, d3, d7) order of the staged f16 queries.
+//  * INT4: B = (n - 8) * gs in f16, exact (|.| <= 2040).
+//  * TQ3: level * 4 = 4 code + 2 corr - 15 (NOCORR: 4 code - 14) is an
+//    integer in [-15, 15]; with gs = 16 gs_hi + gs_lo, B_lo = L * gs_lo and
+//    B_hi = L * 16 gs_hi are exact in f16 and go through separate MFMAs.
+// Each B is decoded once per (tile block, K-step) and used by every query
+// block; queries are f16 hi + lo as on the INT4 path.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v8h as_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(v8h, make_uint4(a, b, c, d));
+}
+
+// Tile u's 16-B chunk `chunk` in a wave region filled by fetch_tiles_lds.
+__device__ __forceinline__ const uint4* tile_chunk(const uint4* region, uint32_t u, uint32_t chunk) {
+    return region + 8u * u + (chunk ^ (u & 7u));
+}
+
+template <int CLS>
+__device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t group,
+                                                const uint16_t* qh, const float* qexp,
+                                                const uint32_t* qsl, float* __restrict__ out,
+                                                uint32_t n_tok, uint32_t tile0) {
+    const uint32_t lane = threadIdx.x & 63u, c = lane & 15u, h = lane >> 4;
+    const uint32_t nrb = (group + 15u) >> 4;  // 2..4 query blocks
+    uint32_t lat[4][4], gsw[4][2];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const uint32_t u = 16u * cb + c;
+        if constexpr (CLS == kClsInt4) {
+            const uint4 x = *tile_chunk(region, u, h);
+            lat[cb][0] = x.x, lat[cb][1] = x.y, lat[cb][2] = x.z, lat[cb][3] = x.w;
+        } else {  // TQ3: code dwords 3h .. 3h+2, correction dword 12 + h
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t d = i < 3 ? 3u * h + i : 12u + h;
+                lat[cb][i] = reinterpret_cast<const uint32_t*>(tile_chunk(region, u, d >> 2))[d & 3u];
+            }
+        }
+        const uint2 g = reinterpret_cast<const uint2*>(tile_chunk(region, u, 7))[1];
+        gsw[cb][0] = g.x, gsw[cb][1] = g.y;
+    }
+    const uint32_t flags0 = reinterpret_cast<const uint32_t*>(tile_chunk(region, 0, 7))[1] >> 16;
+    const bool nocorr = (flags0 & kFlagNoCorr) != 0;  // uniform: the wave is one codec
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    const v2h k_lo = v2h{(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const v2h k_sixteenth = v2h{(_Float16)0.0625f, (_Float16)0.0625f};
+    const v2h k_hi = v2h{(_Float16)-72.0f, (_Float16)-72.0f};
+    const _Float16 tq_off = nocorr ? (_Float16)-1038.0f : (_Float16)-1039.0f;  // 1024 + 14 / 15
+    const v2h k_tq = v2h{tq_off, tq_off};
+    v4f acc[4][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const uint32_t p = 4u * h + ks;  // latent dword (8 dims) this lane covers
+        v8h ahi[4], alo[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const uint32_t row = 16u * rb + c;
+            const bool ok = row < group;
+            const uint16_t* qa = qh + (ok ? row : 0u) * kQStrideH + 16u * p;
+            uint4 x = *reinterpret_cast<const uint4*>(qa);
+            uint4 y = *reinterpret_cast<const uint4*>(qa + 8);
+            if (!ok) x = y = make_uint4(0u, 0u, 0u, 0u);
+            ahi[rb] = __builtin_bit_cast(v8h, x);
+            alo[rb] = __builtin_bit_cast(v8h, y);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const uint32_t gi = 2u * h + (ks >> 1);  // group of dword p
+            const uint32_t gs = (gsw[cb][gi >> 2] >> (8u * (gi & 3u))) & 0xFFu;
+            if constexpr (CLS == kClsInt4) {
+                const _Float16 gh = (_Float16)(float)gs;
+                const v2h g2 = v2h{gh, gh};
+                const uint32_t x = lat[cb][ks], x8 = x >> 8;
+                const v2h l0 = (as_v2h((x & 0x000F000Fu) | magic) + k_lo) * g2;
+                const v2h l1 = __builtin_elementwise_fma(as_v2h((x & 0x00F000F0u) | magic),
+                                                         k_sixteenth, k_hi) * g2;
+                const v2h l2 = (as_v2h((x8 & 0x000F000Fu) | magic) + k_lo) * g2;
+                const v2h l3 = __builtin_elementwise_fma(as_v2h((x8 & 0x00F000F0u) | magic),
+                                                         k_sixteenth, k_hi) * g2;
+                const v8h b = as_v8h(__builtin_bit_cast(uint32_t, l0), __builtin_bit_cast(uint32_t, l1),
+                                     __builtin_bit_cast(uint32_t, l2), __builtin_bit_cast(uint32_t, l3));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    if ((uint32_t)rb < nrb) {
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], b, acc[rb][cb], 0, 0, 0);
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], b, acc[rb][cb], 0, 0, 0);
+                    }
+                }
+            } else {
+                // 24 code bits of dims 8p .. 8p+7 (bit 3i = dim 8p+i) from the
+                // lane's 96 code bits, and their 8 correction bits
+                const uint32_t x = ks == 0 ? lat[cb][0]
+                                 : ks == 1 ? __builtin_amdgcn_alignbit(lat[cb][1], lat[cb][0], 24)
+                                 : ks == 2 ? __builtin_amdgcn_alignbit(lat[cb][2], lat[cb][1], 16)
+                                           : lat[cb][2] >> 8;
+                const uint32_t cr = nocorr ? 0u : (lat[cb][3] >> (8 * ks)) & 0xFFu;
+                uint32_t pr[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // (dim i, dim i + 4): 4 code + 2 corr in the low / high half
+                    const uint32_t v0 = (((x >> (3 * i)) & 7u) << 2) | (((cr >> i) & 1u) << 1);
+                    const uint32_t v1 = (((x >> (3 * i + 12)) & 7u) << 2) | (((cr >> (i + 4)) & 1u) << 1);
+                    pr[i] = __builtin_bit_cast(uint32_t, as_v2h((v0 | (v1 << 16)) | magic) + k_tq);
+                }
+                const _Float16 glo = (_Float16)(float)(gs & 15u);
+                const _Float16 ghi = (_Float16)(float)(gs & 0xF0u);
+                const v2h g_lo = v2h{glo, glo}, g_hi = v2h{ghi, ghi};
+                const v8h blo = as_v8h(
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[0]) * g_lo),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[1]) * g_lo),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[2]) * g_lo),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[3]) * g_lo));
+                const v8h bhi = as_v8h(
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[0]) * g_hi),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[1]) * g_hi),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[2]) * g_hi),
+                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[3]) * g_hi));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    if ((uint32_t)rb < nrb) {
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], blo, acc[rb][cb], 0, 0, 0);
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], blo, acc[rb][cb], 0, 0, 0);
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], bhi, acc[rb][cb], 0, 0, 0);
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], bhi, acc[rb][cb], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // Epilogue: lane L owns tiles u = 16 cb + L % 16 and queries q = 16 rb + 4h + r.
+    const float lvl = CLS == kClsInt4 ? 1.0f : 0.25f;  // TQ3 levels were scaled by 4
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const uint32_t u = 16u * cb + c;
+        const uint32_t t = tile0 + u;
+        const uint4 m6 = *tile_chunk(region, u, 6);
+        const uint4 m7 = *tile_chunk(region, u, 7);
+        const uint4 r0 = *tile_chunk(region, u, 4);
+        const uint4 r1 = *tile_chunk(region, u, 5);
+        const float s255 = __uint_as_float(m6.x) * (1.0f / 255.0f) * lvl;
+        const float lambda = __uint_as_float(m6.y);
+        const bool warm = ((m7.y >> 16) & kFlagWarm) != 0;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if ((uint32_t)rb >= nrb) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t q = 16u * rb + 4u * h + r;
+                if (q >= group) continue;
+                const uint4 s0 = reinterpret_cast<const uint4*>(qsl + 8u * q)[0];
+                const uint4 s1 = reinterpret_cast<const uint4*>(qsl + 8u * q)[1];
+                const uint32_t hd = __popc(r0.x ^ s0.x) + __popc(r0.y ^ s0.y) + __popc(r0.z ^ s0.z) +
+                                    __popc(r0.w ^ s0.w) + __popc(r1.x ^ s1.x) + __popc(r1.y ^ s1.y) +
+                                    __popc(r1.z ^ s1.z) + __popc(r1.w ^ s1.w);
+                float sc = acc[rb][cb][r] * (s255 * qexp[q]);
+                if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)hd, sc);
+                if (t < n_tok) out[(size_t)q * n_tok + t] = sc;
+            }
+        }
+    }
+}
+
+// Dynamic LDS of score_rows_wide_kernel: f16 hi/lo queries, their 2^e
+// factors and the queries' sign words (no f32 copy).
+__host__ __device__ constexpr size_t wide_staging_bytes(uint32_t group) {
+    return (size_t)staging_rows(group) * (kQStrideH * 2u + 4u) + (size_t)group * 32u;
+}
+
+// Scoring of tile rows for 16 < group <= kMfmaMaxGroup: the coalesced tile
+// fetch of score_rows_fast_kernel; INT4 and TQ3 waves run score_wave_wide,
+// waves of other codecs the per-lane path.
+__global__ __launch_bounds__(256) void score_rows_wide_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float cb[16];
+    __shared__ uint4 tile_lds[4][512];
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_staging_bytes(group)
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t rows_alloc = staging_rows(group);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
+    float* qexp = reinterpret_cast<float*>(q16 + rows_alloc * kQStrideH);
+    uint32_t* qsl = reinterpret_cast<uint32_t*>(qexp + rows_alloc);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
+    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+    stage_codebook(cb);
+    stage_queries_f16(qc, qrow0, group, q16, qexp);
+    for (uint32_t i = threadIdx.x; i < group * 8u; i += blockDim.x) qsl[i] = qs[qrow0 * 8 + i];
+    __syncthreads();
+    uint32_t w[32];
+    fetch_tiles_readback(tile_lds[wave], w);
+    const uint32_t t = wave0 + (threadIdx.x & 63u);
+    const bool valid = t < n_tok;
+    float* out = scores + qrow0 * n_tok;
+    const int cls = valid ? codec_class(w[29] >> 16) : -1;
+    const int c0 = __builtin_amdgcn_readfirstlane(cls);
+    const bool uniform = c0 >= 0 && __all(cls == c0 || cls < 0);
+    if (uniform && c0 == kClsInt4) {
+        score_wave_wide<kClsInt4>(tile_lds[wave], group, q16, qexp, qsl, out, n_tok, wave0);
+        return;
+    }
+    if (uniform && c0 == kClsTQ3) {
+        score_wave_wide<kClsTQ3>(tile_lds[wave], group, q16, qexp, qsl, out, n_tok, wave0);
+        return;
+    }
+    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
+}
+
 // CCOS paged scoring on the fast path (pages of at least 64 tiles, group <=
 // kMfmaMaxGroup): as score_rows_fast_kernel, with each wave's 64 consecutive
 // tokens gathered from one physical page. Block (x, y) covers tokens
@@ -1576,7 +1798,8 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
         else if (group <= kRegStageMaxGroup)
             score_rows_fast_kernel<16><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else
-            score_rows_fast_kernel<0><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores);
+            score_rows_wide_kernel<<<grid, 256, wide_staging_bytes(group), s>>>(tp, n_tok, group,
+                                                                              qc, qsw, scores);
         return hipGetLastError();
     }
     if (exact) {

@@ -149,11 +149,14 @@ def test_score_exact_bit_identical_and_hamming(s, torch, group):
             assert_tol(fast[qi], ref)
 
 
-@pytest.mark.parametrize("group,codec", [(4, 0), (8, 2), (20, 4), (5, None)])
+@pytest.mark.parametrize("group,codec", [(4, 0), (8, 2), (20, 4), (5, None), (24, 0), (64, 1),
+                                         (33, None), (40, "tq3_nocorr"), (17, 2)])
 def test_score_fast_streaming_ragged(s, torch, group, codec):
     # Many workgroups per row, a ragged last wave per row (n_tok not a
-    # multiple of 64) and waves entirely past the end of the row. codec None:
-    # random mixed-codec tiles, so waves fall back to the per-lane path.
+    # multiple of 64) and waves entirely past the end of the row. Groups
+    # past 16 take the wide kernel (INT4 and TQ3 with and without the
+    # correction plane on 16x16x32 MFMA). codec None: random mixed-codec
+    # tiles, so waves fall back to the per-lane path.
     n_rows, n_tok = 8, 50_001
     r = np.random.default_rng(1000 + group)
     if codec is None:
@@ -162,7 +165,11 @@ def test_score_fast_streaming_ragged(s, torch, group, codec):
         g = torch.Generator(device="cuda").manual_seed(group)
         keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
         with s.Model(seed=group) as m:
-            td = s.gpu_encode(m, keys, codec, n_kv_heads=n_rows)
+            td = s.gpu_encode(m, keys, s.CODEC_TQ3 if codec == "tq3_nocorr" else codec,
+                              n_kv_heads=n_rows)
+        if codec == "tq3_nocorr":
+            slots = torch.arange(n_rows * n_tok, dtype=torch.int32, device="cuda")
+            s.gpu_ccos_apply(td, slots, 1)
     q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
     qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
     qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
