@@ -89,6 +89,46 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def cpu_encode_baseline(keys_f32, z, gpu_tiles, threads: int) -> dict:
+    """Keys encoded/s of the scalar restatement of the reference's encode
+    (oracle/slha_oracle.c: quantiser + sign-LSH, mode R), `threads` workers on
+    disjoint chunks of a bounded sample; the sample's tiles must equal the
+    GPU's bytes."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+
+    lib = ctypes.CDLL(str(ROOT / "oracle" / "liboracle_slha.so"))
+    lib.orc_encode_batch.restype = ctypes.c_int
+    lib.orc_encode_batch.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                     ctypes.c_uint16, ctypes.c_void_p]
+    n = len(keys_f32)
+    out = np.zeros((n, 128), np.uint8)
+    zc = np.ascontiguousarray(z, np.float32)
+    chunks = np.array_split(np.arange(n), threads)
+
+    def work(idx):
+        if len(idx) == 0:
+            return 0
+        k = np.ascontiguousarray(keys_f32[idx])
+        o = np.zeros((len(idx), 128), np.uint8)
+        rc = lib.orc_encode_batch(k.ctypes.data, len(idx), 0, 1, zc.ctypes.data, None,
+                                  int(idx[0]), 0, o.ctypes.data)
+        out[idx] = o
+        return rc
+
+    with ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        rcs = list(ex.map(work, chunks))
+        dt = time.perf_counter() - t0
+    if any(rcs):
+        raise RuntimeError("oracle encode failed")
+    if not np.array_equal(out, gpu_tiles):
+        raise RuntimeError("CPU encode of the sample differs from the GPU tiles")
+    return {"value": n / dt, "unit": "keys/s", "cores": threads, "kind": "port",
+            "sample": f"{n} C2 keys (head 0, tokens 0..{n - 1}), INT4 mode R; tiles equal the GPU's"}
+
+
 def cpu_baseline(tiles_np, qc_np, qs_np, threads: int) -> dict:
     """Time the reference's CPU compute_score dispatch (restated in C) on a
     bounded sample: whole C2 steps, repeated; median of 5 after a warm-up."""
@@ -489,6 +529,12 @@ def main() -> int:
         threads = max(1, min(threads, 16))
         result["cpu_baseline"] = cpu_baseline(sets[0].cpu().numpy(), qc.cpu().numpy(),
                                               qs.cpu().numpy(), threads)
+        # keys encoded/s on the CPU: the first 32768 keys of head 0 of the
+        # encode-timing key set, compared with the GPU's tiles of those keys
+        z, _ = model.projection()
+        n_cpu = 32768
+        result["cpu_baseline"]["encode"] = cpu_encode_baseline(
+            keys[0, :n_cpu].float().cpu().numpy(), z, enc_out[0, :n_cpu].cpu().numpy(), threads)
     model.release()
     print(json.dumps(result), flush=True)
     return 0
