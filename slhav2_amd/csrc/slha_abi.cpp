@@ -118,6 +118,14 @@ float sqrt_half_pi() { return std::sqrt(kPi / 2.0f); }          // learned.rs:30
 // ---------------------------------------------------------------------------
 // Models
 
+// Device copies of a model's projection on one device.
+struct DeviceProjection {
+    const float* z = nullptr;     // [256][128] f32
+    const float* diag = nullptr;  // [128] +-1, or null without RHT
+    const void* zpack = nullptr;  // kZPackBytes, MFMA operand pack of Z
+    float cert_scale = 0.0f;      // build_projection_pack's scale
+};
+
 struct Model {
     size_t d = 128;
     uint64_t seed = 0;
@@ -126,40 +134,42 @@ struct Model {
     std::vector<float> z;     // [256][128]
     std::vector<float> diag;  // [128], +-1
     std::mutex mu;
-    std::unordered_map<int, std::pair<float*, float*>> dev;
+    std::unordered_map<int, std::pair<DeviceProjection, void*>> dev;  // (views, allocation)
 
     ~Model() {
         for (auto& kv : dev) {
             int cur = 0;
             if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(kv.first) == hipSuccess) {
-                (void)hipFree(kv.second.first);
                 (void)hipFree(kv.second.second);
                 (void)hipSetDevice(cur);
             }
         }
     }
 
-    // Device copies of (Z, diag-or-null) on the current device.
-    std::pair<const float*, const float*> device_buffers() {
+    // Z, its MFMA pack and the RHT diagonal on the current device, in one
+    // allocation made on first use.
+    DeviceProjection device_buffers() {
         int device = 0;
         check_hip(hipGetDevice(&device), "hipGetDevice");
         std::lock_guard<std::mutex> lock(mu);
         auto it = dev.find(device);
         if (it == dev.end()) {
-            float* zd = nullptr;
-            float* dd = nullptr;
-            check_hip(hipMalloc(&zd, z.size() * sizeof(float)), "hipMalloc(Z)");
-            check_hip(hipMemcpy(zd, z.data(), z.size() * sizeof(float), hipMemcpyHostToDevice),
-                      "hipMemcpy(Z)");
-            if (rht) {
-                check_hip(hipMalloc(&dd, diag.size() * sizeof(float)), "hipMalloc(diag)");
-                check_hip(hipMemcpy(dd, diag.data(), diag.size() * sizeof(float),
-                                    hipMemcpyHostToDevice),
-                          "hipMemcpy(diag)");
-            }
-            it = dev.emplace(device, std::make_pair(zd, dd)).first;
+            const size_t zb = z.size() * sizeof(float);
+            std::vector<char> host(zb + kZPackBytes + 128 * sizeof(float));
+            std::memcpy(host.data(), z.data(), zb);
+            DeviceProjection p;
+            p.cert_scale = build_projection_pack(z.data(), host.data() + zb);
+            if (rht) std::memcpy(host.data() + zb + kZPackBytes, diag.data(), 128 * sizeof(float));
+            char* buf = nullptr;
+            check_hip(hipMalloc(&buf, host.size()), "hipMalloc(projection)");
+            check_hip(hipMemcpy(buf, host.data(), host.size(), hipMemcpyHostToDevice),
+                      "hipMemcpy(projection)");
+            p.z = reinterpret_cast<const float*>(buf);
+            p.zpack = buf + zb;
+            p.diag = rht ? reinterpret_cast<const float*>(buf + zb + kZPackBytes) : nullptr;
+            it = dev.emplace(device, std::make_pair(p, static_cast<void*>(buf))).first;
         }
-        return {it->second.first, it->second.second};
+        return it->second.first;
     }
 };
 
@@ -418,7 +428,7 @@ int32_t slha_prepare_query(const SlhaModel* model, const float* q, size_t d, flo
         float* qcd = reinterpret_cast<float*>(base + 512);
         uint64_t* qsd = reinterpret_cast<uint64_t*>(base + 1024);
         check_hip(hipMemcpyAsync(qd, qv.data(), 512, hipMemcpyHostToDevice, s), "H2D q");
-        check_hip(launch_prepare_queries(qd, kDtypeF32, 1, zb.first, zb.second, rht_inv(), qcd, qsd, s),
+        check_hip(launch_prepare_queries(qd, kDtypeF32, 1, zb.z, zb.diag, rht_inv(), qcd, qsd, s),
                   "prepare kernel");
         float qc[128];
         uint64_t qs[4];
@@ -506,7 +516,8 @@ char* slha_audit(void) {
             check_hip(hipMemcpyAsync(base, key, sizeof key, hipMemcpyHostToDevice, s), "H2D key");
             auto zb = m->device_buffers();
             check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, 0, kCodecInt4Single, kResidualZ, 0,
-                                    zb.first, nullptr, lambda_c(), rht_inv(), base + 1024, s),
+                                    zb.z, nullptr, 0.0f, nullptr, lambda_c(), rht_inv(), base + 1024,
+                                    s),
                       "encode kernel");
             SciRustSlhaTile t;
             check_hip(hipMemcpyAsync(&t, base + 1024, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
@@ -590,7 +601,8 @@ int32_t slha_encode_key(const SlhaModel* model, const float* key, size_t d, uint
         char* base = staging(1024, &s);
         check_hip(hipMemcpyAsync(base, kv.data(), 512, hipMemcpyHostToDevice, s), "H2D key");
         check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, position, codec, m->residual_mode, 0,
-                                zb.first, zb.second, lambda_c(), rht_inv(), base + 512, s),
+                                zb.z, zb.zpack, zb.cert_scale, zb.diag, lambda_c(), rht_inv(),
+                                base + 512, s),
                   "encode kernel");
         SciRustSlhaTile t;
         check_hip(hipMemcpyAsync(&t, base + 512, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
@@ -613,7 +625,7 @@ static int32_t decode_common(const SlhaModel* model, const SciRustSlhaTile* tile
         hipStream_t s;
         char* base = staging(1024, &s);
         check_hip(hipMemcpyAsync(base, &t, sizeof t, hipMemcpyHostToDevice, s), "H2D tile");
-        const float* z = (with_residual && !m->rht) ? zb.first : nullptr;
+        const float* z = (with_residual && !m->rht) ? zb.z : nullptr;
         check_hip(launch_decode(base, 1, z, sqrt_half_pi(), reinterpret_cast<float*>(base + 512), s),
                   "decode kernel");
         float v[128];
@@ -710,8 +722,9 @@ int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t ke
         require_device();
         auto zb = m->device_buffers();
         check_hip(launch_encode(keys_dev, key_dtype, n, (uint32_t)n_tok, (uint32_t)n_kv_heads, pos0,
-                                codec, m->residual_mode, warm, zb.first, zb.second, lambda_c(),
-                                rht_inv(), tiles_dev, static_cast<hipStream_t>(stream)),
+                                codec, m->residual_mode, warm, zb.z, zb.zpack, zb.cert_scale,
+                                zb.diag, lambda_c(), rht_inv(), tiles_dev,
+                                static_cast<hipStream_t>(stream)),
                   "encode kernel");
     });
 }
@@ -728,7 +741,7 @@ int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int3
             fail(SLHA_ERR_NULL, "slha_gpu_prepare_queries received a NULL pointer");
         require_device();
         auto zb = m->device_buffers();
-        check_hip(launch_prepare_queries(q_dev, q_dtype, n_q, zb.first, zb.second, rht_inv(),
+        check_hip(launch_prepare_queries(q_dev, q_dtype, n_q, zb.z, zb.diag, rht_inv(),
                                          q_coarse_dev, q_sign_dev, static_cast<hipStream_t>(stream)),
                   "prepare kernel");
     });
@@ -775,7 +788,7 @@ int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev
         if (!tiles_dev || !out_dev) fail(SLHA_ERR_NULL, "slha_gpu_decode received a NULL pointer");
         require_device();
         auto zb = m->device_buffers();
-        const float* z = (with_residual && !m->rht) ? zb.first : nullptr;
+        const float* z = (with_residual && !m->rht) ? zb.z : nullptr;
         check_hip(launch_decode(tiles_dev, n, z, sqrt_half_pi(), out_dev,
                                 static_cast<hipStream_t>(stream)),
                   "decode kernel");

@@ -14,8 +14,11 @@
 #include "slha_device.h"
 #include "slha_launch.h"
 
+#include <algorithm>
 #include <climits>
+#include <cmath>
 #include <cstdlib>
+#include <cstring>
 
 namespace slha {
 
@@ -1349,11 +1352,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(
 // ---------------------------------------------------------------------------
 // Encode: Rust numeric semantics.
 
-__device__ __forceinline__ int32_t rs_i32(float f) {  // `f as i32`
-    if (isnan(f)) return 0;
-    if (f >= 2147483648.0f) return INT_MAX;
-    if (f <= -2147483648.0f) return INT_MIN;
-    return (int32_t)f;
+// `f as i32`: truncation, saturating at the i32 range, NaN -> 0. That is
+// exactly what v_cvt_i32_f32 does, so one instruction replaces the branches.
+__device__ __forceinline__ int32_t rs_i32(float f) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+    return r;
 }
 __device__ __forceinline__ uint32_t rs_u8(float f) {  // `f as u8`
     if (isnan(f)) return 0u;
@@ -1660,6 +1664,283 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
     out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
 }
 
+// ---------------------------------------------------------------------------
+// Encode, mode R, with the sign sketch on MFMA.
+//
+// Bit s of the sketch is (p_seq < 0), where p_seq = sum_k Z[s][k] v[k] is the
+// reference's sequential f32 sum (scenario.rs:70-83). The kernel approximates
+// every projection of a wave's 64 keys with v_mfma_f32_16x16x32_bf16 on a
+// two-term RNE bf16 split of both operands, v = vh + vm + rv and
+// z = zh + zm + rz with |rv| <= 2^-16 |v|, |rz| <= 2^-16 |z|:
+//     p~ = sum_k (zh vh + zh vm + zm vh)
+// With S = sum_k |z_k v_k| <= ||z_s|| ||v||, |p~ - p_seq| is at most
+//     dropped split terms        3.04 * 2^-16 * S        = 4.64e-5 S
+//     MFMA f32 accumulation      384 * 2^-22 * 1.016 S   = 9.30e-5 S
+//                                (384 exact bf16 products; twice the f32
+//                                 unit per addition, for any summation order)
+//     reference sequential sum   gamma_128 = 7.63e-6 S
+// which kEncCertRel = 1.5e-4 covers, plus 2^-100 for underflow. A bit whose
+// |p~| does not exceed the bound is recomputed sequentially from the exact v
+// (kept in LDS), so every bit equals the reference's. With N(0,1)-like
+// residuals about one key in four has one such bit.
+//
+// Layout: one workgroup of 4 waves, one key per lane for the codec part (the
+// same code as encode_kernel), then per wave a 16x16x32 MFMA grid with Z rows
+// as M (16 rows per block sb) and the wave's keys as N (16 per block kb):
+// lane L (c = L%16, g = L/16) supplies row 16sb+c of Z and column 16kb+c of v
+// for dims 32ks+8g..+7 and receives p~ for bits 16sb+4g+r, r = 0..3, of key
+// 16kb+c.
+
+constexpr uint32_t kEncQueue = 256;  // fallback (key, bit) entries per wave
+
+struct EncWaveLds {
+    float v[64 * kDC];       // exact v, row = key, 16-B chunk q at q ^ (key & 7)
+    uint32_t bits[64 * 8];   // sketch words of each key
+    float bound[64];         // certification bound of each key (< 0: all bits certain)
+    uint32_t full[64];       // 1: the key's 256 bits are recomputed sequentially
+    uint32_t queue[kEncQueue];
+    uint32_t count;
+};
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float* enc_chunk(EncWaveLds& w, uint32_t key, uint32_t q) {
+    return &w.v[key * kDC + 4u * (q ^ (key & 7u))];
+}
+
+// RNE bf16 split of two floats: hi = bf16(a, b), mid = bf16((a, b) - hi).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& mid) {
+    const v2f x = {a, b};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2bf));
+    const v2f r = {a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u)};
+    mid = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, v2bf));
+}
+
+template <int CODEC>
+__global__ __launch_bounds__(256) void encode_mfma_kernel(
+    const void* __restrict__ keys, int dtype, uint64_t n_keys, uint32_t n_tok, uint32_t n_kv,
+    uint32_t pos0, int warm, const float* __restrict__ z, const uint4* __restrict__ zpack,
+    float cert_scale, const float* __restrict__ diag, float lambda_c, float rht_inv,
+    uint4* __restrict__ tiles) {
+    __shared__ __align__(16) EncWaveLds lds_all[4];
+    const uint32_t lane = threadIdx.x & 63u;
+    EncWaveLds& W = lds_all[threadIdx.x >> 6];
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool valid = i < n_keys;
+
+    // Codec part, one lane per key: identical arithmetic to encode_kernel.
+    {
+        float v[kDC];
+        float bound = -1.0f;
+        uint32_t full = 0u;
+        if (valid) {
+            const uint32_t row = (uint32_t)(i / n_tok);
+            const uint32_t t = (uint32_t)(i - (uint64_t)row * n_tok);
+            load_vec128(keys, dtype, i, v);
+            uint32_t lw[16], gsw[2];
+            float scale;
+            const uint32_t codec_flag = quantize<CODEC>(v, lw, &scale, gsw);
+            bool finite = true;
+            double acc = 0.0;
+#pragma unroll
+            for (int d = 0; d < kDC; ++d) {
+                v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, scale, d);
+                finite = finite && isfinite(v[d]);
+                const double x = (double)v[d];
+                acc = fma(x, x, acc);
+            }
+            const float sigma = finite ? (float)sqrt(acc / 128.0) : __uint_as_float(0x7FC00000u);
+            if (diag) rht128(v, diag, rht_inv);
+            // ||RHT(e)|| = ||e|| up to ~2^-20; the 2^-10 margin covers it and
+            // the rounding of this bound.
+            const float nv = (float)sqrt(acc);
+            if (!finite || !(nv <= 0x1p100f)) {
+                full = 1u;
+            } else if (acc > 0.0) {
+                bound = nv * 1.0009765625f * cert_scale + 0x1p-100f;
+            }  // acc == 0: v is all +-0, every sum is +0 and every bit 0
+            const uint32_t flags = codec_flag | (warm ? kFlagWarm : 0u);
+            const uint32_t pos = pos0 + t;
+            uint4* out = tiles + i * 8;
+            out[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            out[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+            out[2] = make_uint4(lw[8], lw[9], lw[10], lw[11]);
+            out[3] = make_uint4(lw[12], lw[13], lw[14], lw[15]);
+            out[6] = make_uint4(__float_as_uint(scale), __float_as_uint(sigma * lambda_c),
+                                __float_as_uint(sigma), pos);
+            out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
+        } else {
+#pragma unroll
+            for (int d = 0; d < kDC; ++d) v[d] = 0.0f;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 32; ++q)
+            *reinterpret_cast<float4*>(enc_chunk(W, lane, q)) =
+                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        *reinterpret_cast<uint4*>(&W.bits[lane * 8]) = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(&W.bits[lane * 8 + 4]) = make_uint4(0u, 0u, 0u, 0u);
+        W.bound[lane] = bound;
+        W.full[lane] = full;
+        if (lane == 0) W.count = 0u;
+    }
+    __syncthreads();
+
+    // MFMA part.
+    const uint32_t c = lane & 15u, g = lane >> 4;
+    uint32_t bh[4][4][4], bm[4][4][4];  // [kb][ks][dword] of the B operands
+    float bk[4];
+    uint32_t fk[4];
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; ++kb) {
+        const uint32_t key = 16u * kb + c;
+        bk[kb] = W.bound[key];
+        fk[kb] = W.full[key];
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks) {
+            const float4 x0 = *reinterpret_cast<const float4*>(enc_chunk(W, key, 8u * ks + 2u * g));
+            const float4 x1 = *reinterpret_cast<const float4*>(enc_chunk(W, key, 8u * ks + 2u * g + 1u));
+            split2(x0.x, x0.y, bh[kb][ks][0], bm[kb][ks][0]);
+            split2(x0.z, x0.w, bh[kb][ks][1], bm[kb][ks][1]);
+            split2(x1.x, x1.y, bh[kb][ks][2], bm[kb][ks][2]);
+            split2(x1.z, x1.w, bh[kb][ks][3], bm[kb][ks][3]);
+        }
+    }
+    const uint4* zp = zpack + lane;
+    uint32_t wp[4] = {0u, 0u, 0u, 0u};
+    // Z operands of block sb; the next block's are in flight while this one
+    // is multiplied.
+    uint4 ah[4], am[4], nh[4], nm[4];
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ++ks) {
+        ah[ks] = zp[(ks * 2u + 0u) * 64u];
+        am[ks] = zp[(ks * 2u + 1u) * 64u];
+    }
+#pragma unroll 2
+    for (uint32_t sb = 0; sb < 16; ++sb) {
+        const uint32_t sn = sb + 1u < 16u ? sb + 1u : sb;
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks) {
+            nh[ks] = zp[((sn * 4u + ks) * 2u + 0u) * 64u];
+            nm[ks] = zp[((sn * 4u + ks) * 2u + 1u) * 64u];
+        }
+        v4f acc[4];
+#pragma unroll
+        for (uint32_t kb = 0; kb < 4; ++kb) acc[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        // Four independent accumulation chains, interleaved.
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks) {
+            const v8bf a_h = __builtin_bit_cast(v8bf, ah[ks]);
+            const v8bf a_m = __builtin_bit_cast(v8bf, am[ks]);
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; ++kb) {
+                const v8bf b_h = __builtin_bit_cast(
+                    v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_h, acc[kb], 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; ++kb) {
+                const v8bf b_m = __builtin_bit_cast(
+                    v8bf, make_uint4(bm[kb][ks][0], bm[kb][ks][1], bm[kb][ks][2], bm[kb][ks][3]));
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_m, acc[kb], 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; ++kb) {
+                const v8bf b_h = __builtin_bit_cast(
+                    v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_m, b_h, acc[kb], 0, 0, 0);
+            }
+        }
+        uint32_t unc_any = 0u;
+        uint32_t unc[4];
+#pragma unroll
+        for (uint32_t kb = 0; kb < 4; ++kb) {
+            uint32_t nib = 0u, u = 0u;
+#pragma unroll
+            for (uint32_t r = 0; r < 4; ++r) {
+                nib |= (acc[kb][r] < 0.0f ? 1u : 0u) << r;
+                u |= (fabsf(acc[kb][r]) > bk[kb] ? 0u : 1u) << r;
+            }
+            unc[kb] = fk[kb] ? 0u : u;
+            unc_any |= unc[kb];
+            const uint32_t sh = 4u * g + ((sb & 1u) ? 16u : 0u);
+            wp[kb] = ((sb & 1u) ? wp[kb] : 0u) | (nib << sh);
+            if (sb & 1u) atomicOr(&W.bits[(16u * kb + c) * 8u + (sb >> 1)], wp[kb]);
+        }
+        if (unc_any != 0u) {  // rare: queue the uncertain (key, bit) pairs
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; ++kb) {
+                const uint32_t key = 16u * kb + c;
+                uint32_t u = unc[kb];
+                while (u != 0u) {
+                    const uint32_t r = __builtin_ctz(u);
+                    u &= u - 1u;
+                    const uint32_t slot = atomicAdd(&W.count, 1u);
+                    if (slot < kEncQueue)
+                        W.queue[slot] = (key << 8) | (16u * sb + 4u * g + r);
+                    else
+                        W.full[key] = 1u;
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks) {
+            ah[ks] = nh[ks];
+            am[ks] = nm[ks];
+        }
+    }
+    __syncthreads();
+
+    // Uncertain bits: the reference's sequential sum from the exact v.
+    const uint32_t n_q = min(W.count, kEncQueue);
+    for (uint32_t e = lane; e < n_q; e += 64u) {
+        const uint32_t ent = W.queue[e];
+        const uint32_t key = ent >> 8, s = ent & 255u;
+        if (W.full[key]) continue;
+        const float4* zr = reinterpret_cast<const float4*>(z + (size_t)s * kDC);
+        float acc = 0.0f;
+#pragma unroll 4
+        for (uint32_t q = 0; q < 32; ++q) {
+            const float4 x = *reinterpret_cast<const float4*>(enc_chunk(W, key, q));
+            const float4 zz = zr[q];
+            acc += zz.x * x.x;
+            acc += zz.y * x.y;
+            acc += zz.z * x.z;
+            acc += zz.w * x.w;
+        }
+        const uint32_t m = 1u << (s & 31u);
+        uint32_t* word = &W.bits[key * 8u + (s >> 5)];
+        if (acc < 0.0f)
+            atomicOr(word, m);
+        else
+            atomicAnd(word, ~m);
+    }
+    __syncthreads();
+    if (!valid) return;
+    uint32_t bits[8];
+    if (W.full[lane]) {
+        float v[kDC];
+#pragma unroll
+        for (uint32_t q = 0; q < 32; ++q) {
+            const float4 x = *reinterpret_cast<const float4*>(enc_chunk(W, lane, q));
+            v[4 * q] = x.x;
+            v[4 * q + 1] = x.y;
+            v[4 * q + 2] = x.z;
+            v[4 * q + 3] = x.w;
+        }
+        sign_bits_exact(v, z, bits);
+    } else {
+        const uint4 b0 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8]);
+        const uint4 b1 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8 + 4]);
+        bits[0] = b0.x; bits[1] = b0.y; bits[2] = b0.z; bits[3] = b0.w;
+        bits[4] = b1.x; bits[5] = b1.y; bits[6] = b1.z; bits[7] = b1.w;
+    }
+    uint4* out = tiles + i * 8;
+    out[4] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
+    out[5] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
+}
+
 // Query preparation: q_coarse = q, q_sign = sign(Z * RHT(q)). One workgroup
 // per query and one lane per sign row: every lane forms RHT(q) with identical
 // arithmetic, lane s accumulates row s of Z in the reference order
@@ -1867,16 +2148,61 @@ size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_k
     return rows * nseg * k * 2 * sizeof(uint32_t);
 }
 
+namespace {
+uint16_t bf16_rne(float x) {  // finite x
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float bf16_to_float(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float x;
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+}  // namespace
+
+float build_projection_pack(const float* z, void* pack) {
+    uint16_t* p = static_cast<uint16_t*>(pack);
+    double zmax = 0.0;
+    for (int s = 0; s < kDS; ++s) {
+        double n2 = 0.0;
+        for (int d = 0; d < kDC; ++d) n2 += (double)z[s * kDC + d] * (double)z[s * kDC + d];
+        zmax = std::max(zmax, std::sqrt(n2));
+    }
+    for (int sb = 0; sb < 16; ++sb)
+        for (int ks = 0; ks < 4; ++ks)
+            for (int lane = 0; lane < 64; ++lane)
+                for (int j = 0; j < 8; ++j) {
+                    const int s = 16 * sb + lane % 16, d = 32 * ks + 8 * (lane / 16) + j;
+                    const float x = z[s * kDC + d];
+                    const uint16_t hi = bf16_rne(x);
+                    const uint16_t mid = bf16_rne(x - bf16_to_float(hi));
+                    const size_t o = ((size_t)((sb * 4 + ks) * 2) * 64 + lane) * 8 + j;
+                    p[o] = hi;
+                    p[o + 64 * 8] = mid;
+                }
+    return (float)(kEncCertRel * zmax * (1.0 + 0x1p-20));
+}
+
 hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
                          uint32_t n_kv, uint32_t pos0, int codec, int residual_mode, int warm,
-                         const float* z, const float* diag, float lambda_c, float rht_inv,
-                         void* tiles, hipStream_t s) {
+                         const float* z, const void* zpack, float cert_scale, const float* diag,
+                         float lambda_c, float rht_inv, void* tiles, hipStream_t s) {
     if (n_keys == 0) return hipSuccess;
     const dim3 grid((unsigned)((n_keys + 255) / 256));
     uint4* tp = static_cast<uint4*>(tiles);
-#define SLHA_ENC(C)                                                                         \
-    encode_kernel<C><<<grid, 256, 0, s>>>(keys, dtype, n_keys, n_tok, n_kv, pos0, residual_mode, \
-                                          warm, z, diag, lambda_c, rht_inv, tp)
+    const uint4* zp = static_cast<const uint4*>(zpack);
+    const bool mfma = residual_mode == kResidualR && zp != nullptr;
+#define SLHA_ENC(C)                                                                              \
+    if (mfma)                                                                                    \
+        encode_mfma_kernel<C><<<grid, 256, 0, s>>>(keys, dtype, n_keys, n_tok, n_kv, pos0, warm, \
+                                                   z, zp, cert_scale, diag, lambda_c, rht_inv,  \
+                                                   tp);                                          \
+    else                                                                                         \
+        encode_kernel<C><<<grid, 256, 0, s>>>(keys, dtype, n_keys, n_tok, n_kv, pos0,            \
+                                              residual_mode, warm, z, diag, lambda_c, rht_inv, tp)
     switch (codec) {
         case kCodecInt4Single: SLHA_ENC(kCodecInt4Single); break;
         case kCodecInt4Grouped: SLHA_ENC(kCodecInt4Grouped); break;

@@ -34,10 +34,20 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
 // Device bytes of the `workspace` launch_score_paged_topk needs (top-k candidates).
 size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
                                   uint32_t group, uint32_t k);
+// Mode R computes the sign sketch on MFMA when `zpack` (build_projection_pack)
+// is given, else sequentially per lane; both give the reference's bits.
 hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
                          uint32_t n_kv, uint32_t pos0, int codec, int residual_mode, int warm,
-                         const float* z, const float* diag, float lambda_c, float rht_inv,
-                         void* tiles, hipStream_t s);
+                         const float* z, const void* zpack, float cert_scale, const float* diag,
+                         float lambda_c, float rht_inv, void* tiles, hipStream_t s);
+// Bytes of Z's MFMA operand pack: a two-term bf16 split of [256][128].
+constexpr size_t kZPackBytes = 256 * 128 * 2 * 2;
+// Relative bound on |MFMA projection - sequential f32 projection| per unit
+// ||z_s|| ||v|| (derivation at encode_mfma_kernel).
+constexpr double kEncCertRel = 1.5e-4;
+// Fills `pack` (kZPackBytes, host memory) from Z [256][128] and returns the
+// certification scale kEncCertRel * max_s ||z_s|| the encode launch takes.
+float build_projection_pack(const float* z, void* pack);
 hipError_t launch_prepare_queries(const void* q, int dtype, uint64_t n_q, const float* z,
                                   const float* diag, float rht_inv, float* qc, uint64_t* qs,
                                   hipStream_t s);

@@ -103,6 +103,73 @@ def test_encode_bit_exact(s, torch, codec, rht, kind):
                 assert got.tobytes() == ref.tobytes(), (codec, rht, kind, dtype, r)
 
 
+def near_orthogonal_keys(z, diag, n, seed):
+    """INT4-single keys whose residual e is two dims (a, b) with
+    w[a] e_a + w[b] e_b ~ 0, where w = z[s] (no RHT) or D H z[s] (RHT, so that
+    RHT(e) . z[s] = e . w) for s = key index mod 256: projection s is within
+    rounding of zero, so its sign bit cannot be certified from the MFMA value
+    and goes through the sequential fallback."""
+    import scipy.linalg
+
+    w_all = z.astype(np.float64)
+    if diag is not None:
+        h = scipy.linalg.hadamard(128) / np.sqrt(128.0)
+        w_all = (w_all @ h.T) * diag.astype(np.float64)[None, :]
+    r = np.random.default_rng(seed)
+    k = r.integers(-6, 7, (n, 128)).astype(np.float32)
+    k[:, 0] = 7.0  # max |k| = 7: scale 1, integer dims are exact
+    for i in range(n):
+        w = w_all[i % 256]
+        a, b = sorted(r.choice(np.arange(1, 128), 2, replace=False), key=lambda d: abs(w[d]))
+        ea = r.uniform(0.05, 0.2)
+        k[i, a] += np.float32(ea)
+        k[i, b] += np.float32(-w[a] * ea / w[b])
+    return k
+
+
+@pytest.mark.parametrize("rht", [False, True])
+def test_encode_sign_fallback_paths(s, torch, rht):
+    """The MFMA sign sketch recomputes uncertain bits sequentially. Keys that
+    force each path (per-bit queue, queue overflow to whole-key recompute,
+    non-finite and out-of-range residuals, zero residuals) match the oracle
+    byte for byte."""
+    with s.Model(seed=77, rht=rht) as m:
+        z, diag = m.projection()
+        d = diag if rht else None
+        r = np.random.default_rng(5)
+        blocks = [
+            near_orthogonal_keys(z, d, 512, 6),                    # queue, ~1+ entry per key
+            (r.normal(size=(300, 128)) * 1e-36).astype(np.float32),  # tiny: every bit uncertain
+            (r.normal(size=(64, 128)) * 1e-41).astype(np.float32),   # subnormal keys
+            (r.normal(size=(64, 128)) * 1e37).astype(np.float32),    # |v| beyond 2^100
+            np.zeros((70, 128), np.float32),                        # zero residual
+            np.tile(np.arange(-7, 9, dtype=np.float32), 8)[None].repeat(40, 0),  # exact: e = 0
+            r.normal(size=(200, 128)).astype(np.float32),
+        ]
+        bad = r.normal(size=(64, 128)).astype(np.float32)
+        bad[::3, 5] = np.inf
+        bad[1::3, 77] = np.nan
+        blocks.append(bad)
+        keys = np.concatenate(blocks)
+        for codec in (0, 1, 4, 5):
+            got = tiles_np(s.gpu_encode(m, dev(torch, keys), codec))
+            ref = o.encode(keys, codec, 1, z, d)
+            if got.tobytes() != ref.tobytes():
+                diff = np.nonzero((got.view(np.uint8).reshape(-1, 128) != ref.view(np.uint8).reshape(-1, 128)).any(1))[0]
+                raise AssertionError((codec, rht, diff[:10]))
+
+
+def test_encode_c4_size_bit_exact(s, torch):
+    # C4-like keys (N(0,1) x log-uniform scale, bf16), TQ3 + RHT, 131072 keys:
+    # every tile byte against the oracle.
+    keys = o.bf16_round(keys_for(4242, 131072, "scaled"))
+    with s.Model(seed=0xC4, rht=True) as m:
+        z, diag = m.projection()
+        got = tiles_np(s.gpu_encode(m, dev(torch, keys, torch.bfloat16), s.CODEC_TQ3))
+    ref = o.encode(keys, s.CODEC_TQ3, 1, z, diag)
+    assert got.tobytes() == ref.tobytes()
+
+
 @pytest.mark.parametrize("codec", [0, 2, 4])
 def test_encode_mode_z_and_warm(s, torch, codec):
     keys = keys_for(7, 300)
