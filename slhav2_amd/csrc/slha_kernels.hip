@@ -1680,9 +1680,11 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
 //                                 unit per addition, for any summation order)
 //     reference sequential sum   gamma_128 = 7.63e-6 S
 // which kEncCertRel = 1.5e-4 covers, plus 2^-100 for underflow. A bit whose
-// |p~| does not exceed the bound is recomputed sequentially from the exact v
-// (kept in LDS), so every bit equals the reference's. With N(0,1)-like
-// residuals about one key in four has one such bit.
+// |p~| does not exceed the bound is marked uncertain and recomputed by the
+// key's own lane with the reference's sequential sum over the exact v (kept
+// in LDS), so every bit equals the reference's. With N(0,1)-like residuals a
+// key has about 0.4 uncertain bits. Keys with a non-finite or huge residual
+// (|v| > 2^100) have all 256 bits recomputed.
 //
 // Layout: one workgroup of 4 waves, one key per lane for the codec part (the
 // same code as encode_kernel), then per wave a 16x16x32 MFMA grid with Z rows
@@ -1691,15 +1693,15 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
 // for dims 32ks+8g..+7 and receives p~ for bits 16sb+4g+r, r = 0..3, of key
 // 16kb+c.
 
-constexpr uint32_t kEncQueue = 256;  // fallback (key, bit) entries per wave
+constexpr uint32_t kEncQueue = 256;  // queued (key, bit) recomputations per wave
+constexpr uint32_t kEncQueueKey = 32;  // keys with more uncertain bits keep them
 
 struct EncWaveLds {
     float v[64 * kDC];       // exact v, row = key, 16-B chunk q at q ^ (key & 7)
     uint32_t bits[64 * 8];   // sketch words of each key
-    float bound[64];         // certification bound of each key (< 0: all bits certain)
-    uint32_t full[64];       // 1: the key's 256 bits are recomputed sequentially
-    uint32_t queue[kEncQueue];
-    uint32_t count;
+    uint32_t umask[64 * 8];  // uncertain bits of each key
+    float bound[64];         // certification bound (< 0: all bits certain, inf: none)
+    uint32_t queue[kEncQueue];  // (key << 8) | bit
 };
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -1708,6 +1710,39 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float* enc_chunk(EncWaveLds& w, uint32_t key, uint32_t q) {
     return &w.v[key * kDC + 4u * (q ^ (key & 7u))];
+}
+
+// Bit s of one key with the reference's arithmetic: sequential f32 sum from
+// 0.0 of Z[s][k] * v[k], k = 0..127, no contraction (scenario.rs:70-83).
+__device__ __forceinline__ uint32_t enc_exact_bit(EncWaveLds& w, uint32_t key,
+                                                  const float* __restrict__ zrow) {
+    const float4* zr = reinterpret_cast<const float4*>(zrow);
+    float acc = 0.0f;
+#pragma unroll 4
+    for (uint32_t q = 0; q < 32; ++q) {
+        const float4 x = *reinterpret_cast<const float4*>(enc_chunk(w, key, q));
+        const float4 zz = zr[q];
+        acc += zz.x * x.x;
+        acc += zz.y * x.y;
+        acc += zz.z * x.z;
+        acc += zz.w * x.w;
+    }
+    return acc < 0.0f ? 1u : 0u;
+}
+
+// Inclusive prefix sum of one u32 per lane over the wave (DPP row shifts,
+// then row broadcasts).
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
+#define SLHA_DPP_ADD(ctrl, rows) \
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rows, 0xF, false)
+    SLHA_DPP_ADD(0x111, 0xF);  // row_shr:1
+    SLHA_DPP_ADD(0x112, 0xF);  // row_shr:2
+    SLHA_DPP_ADD(0x114, 0xF);  // row_shr:4
+    SLHA_DPP_ADD(0x118, 0xF);  // row_shr:8
+    SLHA_DPP_ADD(0x142, 0xA);  // row_bcast:15
+    SLHA_DPP_ADD(0x143, 0xC);  // row_bcast:31
+#undef SLHA_DPP_ADD
+    return x;
 }
 
 // RNE bf16 split of two floats: hi = bf16(a, b), mid = bf16((a, b) - hi).
@@ -1734,7 +1769,7 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
     {
         float v[kDC];
         float bound = -1.0f;
-        uint32_t full = 0u;
+        bool full = false;
         if (valid) {
             const uint32_t row = (uint32_t)(i / n_tok);
             const uint32_t t = (uint32_t)(i - (uint64_t)row * n_tok);
@@ -1757,7 +1792,7 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
             // the rounding of this bound.
             const float nv = (float)sqrt(acc);
             if (!finite || !(nv <= 0x1p100f)) {
-                full = 1u;
+                full = true;
             } else if (acc > 0.0) {
                 bound = nv * 1.0009765625f * cert_scale + 0x1p-100f;
             }  // acc == 0: v is all +-0, every sum is +0 and every bit 0
@@ -1781,9 +1816,9 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
                 make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
         *reinterpret_cast<uint4*>(&W.bits[lane * 8]) = make_uint4(0u, 0u, 0u, 0u);
         *reinterpret_cast<uint4*>(&W.bits[lane * 8 + 4]) = make_uint4(0u, 0u, 0u, 0u);
-        W.bound[lane] = bound;
-        W.full[lane] = full;
-        if (lane == 0) W.count = 0u;
+        *reinterpret_cast<uint4*>(&W.umask[lane * 8]) = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(&W.umask[lane * 8 + 4]) = make_uint4(0u, 0u, 0u, 0u);
+        W.bound[lane] = full ? INFINITY : bound;
     }
     __syncthreads();
 
@@ -1791,12 +1826,10 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
     const uint32_t c = lane & 15u, g = lane >> 4;
     uint32_t bh[4][4][4], bm[4][4][4];  // [kb][ks][dword] of the B operands
     float bk[4];
-    uint32_t fk[4];
 #pragma unroll
     for (uint32_t kb = 0; kb < 4; ++kb) {
         const uint32_t key = 16u * kb + c;
         bk[kb] = W.bound[key];
-        fk[kb] = W.full[key];
 #pragma unroll
         for (uint32_t ks = 0; ks < 4; ++ks) {
             const float4 x0 = *reinterpret_cast<const float4*>(enc_chunk(W, key, 8u * ks + 2u * g));
@@ -1808,7 +1841,7 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
         }
     }
     const uint4* zp = zpack + lane;
-    uint32_t wp[4] = {0u, 0u, 0u, 0u};
+    uint32_t wp[4] = {0u, 0u, 0u, 0u}, up[4] = {0u, 0u, 0u, 0u};
     // Z operands of block sb; the next block's are in flight while this one
     // is multiplied.
     uint4 ah[4], am[4], nh[4], nm[4];
@@ -1852,8 +1885,6 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
                 acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_m, b_h, acc[kb], 0, 0, 0);
             }
         }
-        uint32_t unc_any = 0u;
-        uint32_t unc[4];
 #pragma unroll
         for (uint32_t kb = 0; kb < 4; ++kb) {
             uint32_t nib = 0u, u = 0u;
@@ -1862,26 +1893,13 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
                 nib |= (acc[kb][r] < 0.0f ? 1u : 0u) << r;
                 u |= (fabsf(acc[kb][r]) > bk[kb] ? 0u : 1u) << r;
             }
-            unc[kb] = fk[kb] ? 0u : u;
-            unc_any |= unc[kb];
             const uint32_t sh = 4u * g + ((sb & 1u) ? 16u : 0u);
             wp[kb] = ((sb & 1u) ? wp[kb] : 0u) | (nib << sh);
-            if (sb & 1u) atomicOr(&W.bits[(16u * kb + c) * 8u + (sb >> 1)], wp[kb]);
-        }
-        if (unc_any != 0u) {  // rare: queue the uncertain (key, bit) pairs
-#pragma unroll
-            for (uint32_t kb = 0; kb < 4; ++kb) {
-                const uint32_t key = 16u * kb + c;
-                uint32_t u = unc[kb];
-                while (u != 0u) {
-                    const uint32_t r = __builtin_ctz(u);
-                    u &= u - 1u;
-                    const uint32_t slot = atomicAdd(&W.count, 1u);
-                    if (slot < kEncQueue)
-                        W.queue[slot] = (key << 8) | (16u * sb + 4u * g + r);
-                    else
-                        W.full[key] = 1u;
-                }
+            up[kb] = ((sb & 1u) ? up[kb] : 0u) | (u << sh);
+            if (sb & 1u) {
+                const uint32_t w = (16u * kb + c) * 8u + (sb >> 1);
+                atomicOr(&W.bits[w], wp[kb]);
+                if (up[kb] != 0u) atomicOr(&W.umask[w], up[kb]);
             }
         }
 #pragma unroll
@@ -1892,49 +1910,61 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
     }
     __syncthreads();
 
-    // Uncertain bits: the reference's sequential sum from the exact v.
-    const uint32_t n_q = min(W.count, kEncQueue);
-    for (uint32_t e = lane; e < n_q; e += 64u) {
-        const uint32_t ent = W.queue[e];
-        const uint32_t key = ent >> 8, s = ent & 255u;
-        if (W.full[key]) continue;
-        const float4* zr = reinterpret_cast<const float4*>(z + (size_t)s * kDC);
-        float acc = 0.0f;
-#pragma unroll 4
-        for (uint32_t q = 0; q < 32; ++q) {
-            const float4 x = *reinterpret_cast<const float4*>(enc_chunk(W, key, q));
-            const float4 zz = zr[q];
-            acc += zz.x * x.x;
-            acc += zz.y * x.y;
-            acc += zz.z * x.z;
-            acc += zz.w * x.w;
+    // Uncertain bits. Keys with at most kEncQueueKey of them (nearly all)
+    // queue their (key, bit) pairs, and the queue is spread over the wave's
+    // lanes; a key with more (non-finite or huge residual), or whose pairs do
+    // not fit, is finished by its own lane.
+    const uint4 u0 = *reinterpret_cast<const uint4*>(&W.umask[lane * 8]);
+    const uint4 u1 = *reinterpret_cast<const uint4*>(&W.umask[lane * 8 + 4]);
+    const uint32_t um[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    uint32_t n = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 8; ++w) n += __builtin_popcount(um[w]);
+    const uint32_t nq = n <= kEncQueueKey ? n : 0u;
+    const uint32_t incl = wave_inclusive_sum(nq);
+    const bool queued = incl <= kEncQueue;
+    const unsigned long long fit = __ballot(queued);  // lanes 0.. (incl is monotonic)
+    const uint32_t total =
+        fit ? (uint32_t)__builtin_amdgcn_readlane((int)incl, __popcll(fit) - 1) : 0u;
+    if (queued && nq != 0u) {
+        uint32_t e = incl - nq;
+#pragma unroll
+        for (uint32_t w = 0; w < 8; ++w) {
+            uint32_t m = um[w];
+            while (m != 0u) {
+                const uint32_t r = __builtin_ctz(m);
+                m &= m - 1u;
+                W.queue[e++] = (lane << 8) | (32u * w + r);
+            }
         }
-        const uint32_t m = 1u << (s & 31u);
-        uint32_t* word = &W.bits[key * 8u + (s >> 5)];
-        if (acc < 0.0f)
+    }
+    __syncthreads();
+    for (uint32_t e = lane; e < total; e += 64u) {
+        const uint32_t ent = W.queue[e];
+        const uint32_t key = ent >> 8, sbit = ent & 255u;
+        const uint32_t m = 1u << (sbit & 31u);
+        uint32_t* word = &W.bits[key * 8u + (sbit >> 5)];
+        if (enc_exact_bit(W, key, z + (size_t)sbit * kDC))
             atomicOr(word, m);
         else
             atomicAnd(word, ~m);
     }
     __syncthreads();
     if (!valid) return;
-    uint32_t bits[8];
-    if (W.full[lane]) {
-        float v[kDC];
+    const uint4 b0 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8]);
+    const uint4 b1 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8 + 4]);
+    uint32_t bits[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    if (!queued || n > kEncQueueKey) {
 #pragma unroll
-        for (uint32_t q = 0; q < 32; ++q) {
-            const float4 x = *reinterpret_cast<const float4*>(enc_chunk(W, lane, q));
-            v[4 * q] = x.x;
-            v[4 * q + 1] = x.y;
-            v[4 * q + 2] = x.z;
-            v[4 * q + 3] = x.w;
+        for (uint32_t w = 0; w < 8; ++w) {
+            uint32_t m = um[w];
+            while (m != 0u) {
+                const uint32_t r = __builtin_ctz(m);
+                m &= m - 1u;
+                const uint32_t b = enc_exact_bit(W, lane, z + (size_t)(32u * w + r) * kDC);
+                bits[w] = (bits[w] & ~(1u << r)) | (b << r);
+            }
         }
-        sign_bits_exact(v, z, bits);
-    } else {
-        const uint4 b0 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8]);
-        const uint4 b1 = *reinterpret_cast<const uint4*>(&W.bits[lane * 8 + 4]);
-        bits[0] = b0.x; bits[1] = b0.y; bits[2] = b0.z; bits[3] = b0.w;
-        bits[4] = b1.x; bits[5] = b1.y; bits[6] = b1.z; bits[7] = b1.w;
     }
     uint4* out = tiles + i * 8;
     out[4] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
