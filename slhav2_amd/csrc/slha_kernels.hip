@@ -947,8 +947,10 @@ __global__ __launch_bounds__(256) void score_rows_wide_kernel(
 // CCOS paged scoring on the fast path (pages of at least 64 tiles, group <=
 // kMfmaMaxGroup): as score_rows_fast_kernel, with each wave's 64 consecutive
 // tokens gathered from one physical page. Block (x, y) covers tokens
-// [256x, 256x+256) of (sequence s, KV head h), y = s*n_kv + h; token t lives
-// in page page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
+// [256x, 256x+256) of row y = s*n_kv + h (sequence s, KV head h); token t
+// lives in page page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
+// (Token blocks along x keep a row's pages together in time; with rows along
+// x the paged C5 scoring ran 9 % slower.)
 template <uint32_t REG_ROWS>
 __global__ __launch_bounds__(256) void score_paged_fast_kernel(
     const uint4* __restrict__ arena, uint32_t page_shift, const uint32_t* __restrict__ page_table,
@@ -959,18 +961,18 @@ __global__ __launch_bounds__(256) void score_paged_fast_kernel(
     __shared__ uint4 tile_lds[4][512];
     __shared__ __attribute__((aligned(16))) float qstatic[REG_ROWS ? staging_bytes(REG_ROWS) / 4 : 1];
     extern __shared__ __attribute__((aligned(16))) float qlds[];
-    const uint32_t y = blockIdx.y;
+    const uint32_t y = blockIdx.y, bx = blockIdx.x;
     const uint32_t s = y / n_kv, h = y - s * n_kv;
     const uint32_t len = seq_len[s];
-    if (blockIdx.x * blockDim.x >= len) return;  // whole block past this sequence
+    if (bx * blockDim.x >= len) return;  // whole block past this sequence
     const size_t qrow0 = (size_t)y * group;
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = bx * blockDim.x + threadIdx.x;
     const StagedQueries sq =
         carve_staging(REG_ROWS ? qstatic : qlds, REG_ROWS ? REG_ROWS : staging_rows(group));
     QueryRegs<REG_ROWS ? REG_ROWS : 4> qr;
     if constexpr (REG_ROWS > 0) stage_issue<REG_ROWS>(qc, qrow0, group, qr);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
+    const uint32_t wave0 = bx * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < len ? len - wave0 : 0u;
     const uint4* base = arena;
     if (n_valid) {  // 64 | page_tiles: the wave's tokens share one page
@@ -997,10 +999,8 @@ __global__ __launch_bounds__(256) void score_paged_fast_kernel(
 }
 
 // CCOS paged scoring, general case (pages of fewer than 64 tiles, or groups
-// past kMfmaMaxGroup): one lane per token, tiles gathered per lane. Block
-// (x, y) covers tokens [256x, 256x+256) of (sequence s, KV head h) with
-// y = s*n_kv + h; token t lives in physical page
-// page_table[y*max_pages + t/page_tiles] at slot t % page_tiles.
+// past kMfmaMaxGroup): one lane per token, tiles gathered per lane. Blocks
+// map to (token block, row) as in score_paged_fast_kernel.
 __global__ __launch_bounds__(256) void score_paged_kernel(
     const uint4* __restrict__ arena, uint32_t page_shift, const uint32_t* __restrict__ page_table,
     uint32_t max_pages, const uint32_t* __restrict__ seq_len,
@@ -1008,12 +1008,12 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
     const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
     __shared__ float cb[16];
     extern __shared__ __attribute__((aligned(16))) float qlds[];  // staged_rows * kQStride
-    const uint32_t y = blockIdx.y;
+    const uint32_t y = blockIdx.y, bx = blockIdx.x;
     const uint32_t s = y / n_kv, h = y - s * n_kv;
     const uint32_t len = seq_len[s];
-    if (blockIdx.x * blockDim.x >= len) return;  // whole block past this sequence
+    if (bx * blockDim.x >= len) return;  // whole block past this sequence
     const size_t qrow0 = (size_t)y * group;
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = bx * blockDim.x + threadIdx.x;
     const bool valid = t < len;
     uint32_t w[32];
     if (valid) {
@@ -1044,26 +1044,24 @@ __global__ __launch_bounds__(256) void score_paged_kernel(
 // Top-k per score row: score descending, ties to the lower token index.
 //
 // Two stages; each reads its input once, with coalesced branch-free loads:
-//  1. topk_segment_kernel: one 256-thread workgroup per 16384-score segment
-//     of a (sequence, query head) row, 64 scores per thread in registers; its
+//  1. topk_segment_kernel: one 512-thread workgroup per 16384-score segment
+//     of a (sequence, query head) row, 32 scores per thread in registers; its
 //     top k go, sorted, to the row's candidate list (k slots per segment).
-//  2. topk_merge_kernel: one 1024-thread workgroup per row selects the top k
-//     of the row's candidates.
-// Both use block_topk: scores are order-preserving u32 keys; each wave sorts
-// its 64 per-thread maxima (a shuffle bitonic network) and takes the
-// r-th largest, r = ceil(kk / waves); tau = the smallest of those is a lower
+//  2. topk_merge_kernel: one workgroup per row merges the row's sorted
+//     segment lists by rank counting (binary searches).
+// The segments use block_topk: scores are order-preserving u32 keys; each wave
+// extracts the r-th largest of its 64 per-thread maxima (r rounds of a DPP
+// wave maximum), r = ceil(kk / waves); tau = the smallest of those is a lower
 // bound of the kk-th largest key (every wave has r threads holding a key
 // >= tau), so the keys >= tau contain the whole top kk, ties included.
 // They are typically a few times kk: each one's rank in (key desc, index
 // asc) order is counted against the others and ranks < kk are written in
 // that order. When they do not fit in LDS (heavy ties), an exact 8-bit radix
 // select finds the kk-th largest key T and the winners are the keys > T
-// plus the first keys == T in item order (item order is index order among
-// equal keys in both stages).
+// plus the first keys == T in index order.
 
-constexpr int kSegThreads = 256;       // 64 scores per thread (kTopkSeg = 16384)
-constexpr int kTopkThreads = 1024;     // merge workgroup
-constexpr int kMergePer = (int)(kTopkMaxCandidates / kTopkThreads);  // candidates per merge thread
+constexpr int kSegThreads = 512;       // 32 scores per thread (kTopkSeg = 16384)
+constexpr int kMergeThreads = 256;     // merge workgroup
 constexpr uint32_t kTopkCap = 1024;    // candidates ranked in LDS
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -1075,6 +1073,21 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+// Inclusive prefix sum of one u32 per lane over the wave (DPP row shifts,
+// then row broadcasts).
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
+#define SLHA_DPP_ADD(ctrl, rows) \
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rows, 0xF, false)
+    SLHA_DPP_ADD(0x111, 0xF);  // row_shr:1
+    SLHA_DPP_ADD(0x112, 0xF);  // row_shr:2
+    SLHA_DPP_ADD(0x114, 0xF);  // row_shr:4
+    SLHA_DPP_ADD(0x118, 0xF);  // row_shr:8
+    SLHA_DPP_ADD(0x142, 0xA);  // row_bcast:15
+    SLHA_DPP_ADD(0x143, 0xC);  // row_bcast:31
+#undef SLHA_DPP_ADD
+    return x;
+}
+
 // Exclusive prefix sum of one u32 per thread over a workgroup of NT threads
 // (NT a multiple of 64); `tmp` holds NT/64 words of LDS. Returns the
 // exclusive prefix; *total receives the sum. Contains barriers.
@@ -1082,12 +1095,7 @@ template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* tmp,
                                                          uint32_t* total) {
     const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-    uint32_t incl = x;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(incl, off);
-        if (lane >= (uint32_t)off) incl += y;
-    }
+    const uint32_t incl = wave_inclusive_sum(x);
     if (lane == 63) tmp[wv] = incl;
     __syncthreads();
     uint32_t before = 0, all = 0;
@@ -1162,7 +1170,7 @@ __device__ __forceinline__ uint32_t radix_select(Val value, Take take, uint32_t 
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (uint32_t i = threadIdx.x; i < 256u; i += NT) hist[i] = 0u;
         __syncthreads();
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < PER; ++j) {
             const uint32_t v = value(j);
             if (take(j) && (v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
@@ -1180,10 +1188,14 @@ __device__ __forceinline__ uint32_t radix_select(Val value, Take take, uint32_t 
 
 // Top kk (<= kMaxTopK, <= number of valid items) of the workgroup's items:
 // thread t holds items j = 0..PER-1 with key_at(j), index idx_at(j) (unique)
-// and ok_at(j) (valid). Writes the winners, ranked, to out_key/out_idx[0..kk).
+// and ok_at(j) (valid). key_ld/ok_ld give the same from memory for any j;
+// the rare heavy-tie path uses them so that the register copies need not
+// stay alive through it. Writes the winners, ranked, to out_key/out_idx[0..kk).
 // Shared-memory scratch comes from the caller. Every thread calls it.
-template <int NT, int PER, typename KeyAt, typename IdxAt, typename OkAt>
-__device__ __forceinline__ void block_topk(KeyAt key_at, IdxAt idx_at, OkAt ok_at, uint32_t kk,
+template <int NT, int PER, typename KeyAt, typename OkAt, typename KeyLd, typename OkLd,
+          typename IdxAt>
+__device__ __forceinline__ void block_topk(KeyAt key_at, OkAt ok_at, KeyLd key_ld, OkLd ok_ld,
+                                           IdxAt idx_at, uint32_t kk,
                                            uint2* cand, uint32_t* rank, uint32_t* hist,
                                            uint32_t* tmp, uint32_t* sh,
                                            uint32_t* __restrict__ out_key,
@@ -1214,23 +1226,27 @@ __device__ __forceinline__ void block_topk(KeyAt key_at, IdxAt idx_at, OkAt ok_a
     } else {
         // Heavy ties: the kk-th largest key T, then among the keys == T the
         // `need` lowest indices (the largest ~index), both by radix select.
+        // This rare path reads the keys again (key_ld) rather than keeping
+        // the register copies alive, which keeps the common path's register
+        // budget low.
         uint32_t need;
-        const uint32_t thr = radix_select<NT, PER>(key_at, ok_at, kk, hist, tmp, sh, &need);
-        auto is_eq = [&](int j) { return ok_at(j) && key_at(j) == thr; };
+        const uint32_t thr = radix_select<NT, PER>(key_ld, ok_ld, kk, hist, tmp, sh, &need);
+        auto is_eq = [&](int j) { return ok_ld(j) && key_ld(j) == thr; };
         auto inv_idx = [&](int j) { return ~idx_at(j); };
         uint32_t one;
         const uint32_t ithr = need ? radix_select<NT, PER>(inv_idx, is_eq, need, hist, tmp, sh, &one)
                                    : 0xFFFFFFFFu;
         auto win = [&](int j) {
-            return ok_at(j) && (key_at(j) > thr || (need && key_at(j) == thr && ~idx_at(j) >= ithr));
+            const uint32_t kj = key_ld(j);
+            return ok_ld(j) && (kj > thr || (need && kj == thr && ~idx_at(j) >= ithr));
         };
         c = 0;
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < PER; ++j) c += win(j) ? 1u : 0u;
         pos = block_exclusive_scan<NT>(c, tmp, &total);
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < PER; ++j)
-            if (win(j)) cand[pos++] = make_uint2(key_at(j), idx_at(j));
+            if (win(j)) cand[pos++] = make_uint2(key_ld(j), idx_at(j));
     }
     // rank by (key desc, index asc); ranks < kk are the result, in order.
     // Candidate i's rank is summed over `slices` threads, each comparing it
@@ -1268,7 +1284,7 @@ __device__ __forceinline__ void block_topk(KeyAt key_at, IdxAt idx_at, OkAt ok_a
     }
 }
 
-__global__ __launch_bounds__(kSegThreads) void topk_segment_kernel(
+__global__ __launch_bounds__(kSegThreads, 2) void topk_segment_kernel(
     const float* __restrict__ scores, const uint32_t* __restrict__ seq_len,
     const unsigned long long* __restrict__ score_base, uint32_t hq, uint32_t k, uint32_t nseg_max,
     uint32_t* __restrict__ cand_key, uint32_t* __restrict__ cand_idx) {
@@ -1277,11 +1293,11 @@ __global__ __launch_bounds__(kSegThreads) void topk_segment_kernel(
     __shared__ uint32_t sh[2];
     __shared__ uint2 cand[kTopkCap];
     __shared__ uint32_t rank[kTopkCap];
-    const uint32_t row = blockIdx.y;
+    const uint32_t row = blockIdx.x, seg = blockIdx.y;
     const uint32_t s = row / hq, qh = row - s * hq;
     const uint32_t len = seq_len[s];
     const unsigned long long sbase = score_base[s];  // issued with seq_len
-    const uint32_t start = blockIdx.x * kTopkSeg;
+    const uint32_t start = seg * kTopkSeg;
     if (start >= len) return;  // whole segment past this sequence
     const uint32_t n = len - start < kTopkSeg ? len - start : kTopkSeg;
     const uint32_t kk = k < n ? k : n;
@@ -1292,60 +1308,89 @@ __global__ __launch_bounds__(kSegThreads) void topk_segment_kernel(
     const float* sc = scores + sbase + (size_t)qh * len + start;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(sc), 0, __builtin_amdgcn_readfirstlane(n * 4u), 0x00020000);
+    // Key 0 marks an item past the segment: order_key never yields 0 for a
+    // score (it would take the NaN 0xFFFFFFFF, which is raised to key 1).
     uint32_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-        key[j] = order_key(__builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (j * kSegThreads + threadIdx.x) * 4u, 0, 0)));
-    const size_t o = ((size_t)row * nseg_max + blockIdx.x) * k;
+    for (int j = 0; j < PER; ++j) {
+        const uint32_t kj = max(order_key(__builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (j * kSegThreads + threadIdx.x) * 4u, 0, 0))), 1u);
+        key[j] = (uint32_t)j * kSegThreads + threadIdx.x < n ? kj : 0u;
+    }
+    const size_t o = ((size_t)row * nseg_max + seg) * k;
     block_topk<kSegThreads, PER>(
-        [&](int j) { return key[j]; },
-        [&](int j) { return start + (uint32_t)j * kSegThreads + threadIdx.x; },
-        [&](int j) { return (uint32_t)j * kSegThreads + threadIdx.x < n; }, kk, cand, rank, hist,
+        [&](int j) { return key[j]; }, [&](int j) { return key[j] != 0u; },
+        [&](int j) {
+            return max(order_key(__builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, (j * kSegThreads + threadIdx.x) * 4u, 0, 0))), 1u);
+        },
+        [&](int j) { return (uint32_t)j * kSegThreads + threadIdx.x < n; },
+        [&](int j) { return start + (uint32_t)j * kSegThreads + threadIdx.x; }, kk, cand, rank, hist,
         tmp, sh, cand_key + o, cand_idx + o);
 }
 
-__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(
+// Merge of the sorted per-segment lists of a row. Segment g's list holds its
+// top min(k, n_g) scores sorted by (key desc, index asc), and segment g's
+// indices all precede segment g+1's. A candidate's final rank is its position
+// in its own list plus, for every other list, the number of that list's
+// entries that precede it: entries with a larger key, plus entries with an
+// equal key from an earlier segment (binary search, the lists being sorted).
+// Ranks are unique, so candidates with rank < k write themselves in place.
+// The lists live in dynamic LDS (nseg_max * k * 8 bytes, at most 64 KiB).
+__global__ __launch_bounds__(kMergeThreads) void topk_merge_kernel(
     const uint32_t* __restrict__ cand_key, const uint32_t* __restrict__ cand_idx,
     const uint32_t* __restrict__ seq_len, uint32_t hq, uint32_t k, uint32_t nseg_max,
     uint32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t tmp[kTopkThreads / 64];
-    __shared__ uint32_t sh[2];
-    __shared__ uint2 cand[kTopkCap];
-    __shared__ uint32_t rank[kTopkCap];
-    __shared__ uint32_t sel_key[kMaxTopK];
-    __shared__ uint32_t sel_idx[kMaxTopK];
+    extern __shared__ uint32_t merge_lds[];
+    uint32_t* lkey = merge_lds;                      // [nseg_max * k]
+    uint32_t* lidx = merge_lds + (size_t)nseg_max * k;
     const uint32_t row = blockIdx.x;
     const uint32_t s = row / hq;
     const uint32_t len = seq_len[s];
     const uint32_t kk = k < len ? k : len;
     const uint32_t nseg = (len + kTopkSeg - 1) / kTopkSeg;
     const size_t base = (size_t)row * nseg_max * k;
-    // Segment g holds min(k, len - g*kTopkSeg) candidates and every segment
-    // but the last is full, so the valid candidates are [0, m_valid), at most
-    // kTopkMaxCandidates = kTopkThreads * kMergePer.
-    const uint32_t rem_last = nseg ? len - (nseg - 1) * kTopkSeg : 0u;
-    const uint32_t m_valid = nseg ? (nseg - 1) * k + (rem_last < k ? rem_last : k) : 0u;
-    if (kk > 0) {
-        uint32_t key[kMergePer], idx[kMergePer];
-        bool ok[kMergePer];
-#pragma unroll
-        for (int j = 0; j < kMergePer; ++j) {
-            const uint32_t c = j * kTopkThreads + threadIdx.x;
-            ok[j] = c < m_valid;
-            key[j] = ok[j] ? cand_key[base + c] : 0u;
-            idx[j] = ok[j] ? cand_idx[base + c] : 0u;
-        }
-        block_topk<kTopkThreads, kMergePer>(
-            [&](int j) { return key[j]; }, [&](int j) { return idx[j]; },
-            [&](int j) { return ok[j]; }, kk, cand, rank, hist, tmp, sh, sel_key, sel_idx);
+    const uint32_t slots = nseg * k;
+    for (uint32_t c = threadIdx.x; c < slots; c += kMergeThreads) {
+        lkey[c] = cand_key[base + c];
+        lidx[c] = cand_idx[base + c];
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < k; i += kTopkThreads) {
+    auto list_len = [&](uint32_t g) {
+        const uint32_t n = len - g * kTopkSeg;
+        return n < k ? n : k;
+    };
+    for (uint32_t c = threadIdx.x; c < slots; c += kMergeThreads) {
+        const uint32_t g = c / k, p = c - g * k;
+        if (p >= list_len(g)) continue;
+        const uint32_t key = lkey[c];
+        uint32_t rank = p;
+        for (uint32_t h = 0; h < nseg && rank < kk; ++h) {
+            if (h == g) continue;
+            // entries of list h before this candidate: key > K, or key == K
+            // when h is an earlier segment (first position failing that)
+            const uint32_t* lk = lkey + h * k;
+            uint32_t lo = 0, hi = list_len(h);
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                const uint32_t e = lk[mid];
+                if (e > key || (h < g && e == key))
+                    lo = mid + 1;
+                else
+                    hi = mid;
+            }
+            rank += lo;
+        }
+        if (rank < kk) {
+            const size_t oo = (size_t)row * k + rank;
+            topk_idx[oo] = lidx[c];
+            topk_val[oo] = key_to_float(key);
+        }
+    }
+    for (uint32_t i = kk + threadIdx.x; i < k; i += kMergeThreads) {
         const size_t oo = (size_t)row * k + i;
-        topk_idx[oo] = i < kk ? sel_idx[i] : 0xFFFFFFFFu;
-        topk_val[oo] = i < kk ? key_to_float(sel_key[i]) : -INFINITY;
+        topk_idx[oo] = 0xFFFFFFFFu;
+        topk_val[oo] = -INFINITY;
     }
 }
 
@@ -1730,20 +1775,6 @@ __device__ __forceinline__ uint32_t enc_exact_bit(EncWaveLds& w, uint32_t key,
     return acc < 0.0f ? 1u : 0u;
 }
 
-// Inclusive prefix sum of one u32 per lane over the wave (DPP row shifts,
-// then row broadcasts).
-__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
-#define SLHA_DPP_ADD(ctrl, rows) \
-    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rows, 0xF, false)
-    SLHA_DPP_ADD(0x111, 0xF);  // row_shr:1
-    SLHA_DPP_ADD(0x112, 0xF);  // row_shr:2
-    SLHA_DPP_ADD(0x114, 0xF);  // row_shr:4
-    SLHA_DPP_ADD(0x118, 0xF);  // row_shr:8
-    SLHA_DPP_ADD(0x142, 0xA);  // row_bcast:15
-    SLHA_DPP_ADD(0x143, 0xC);  // row_bcast:31
-#undef SLHA_DPP_ADD
-    return x;
-}
 
 // RNE bf16 split of two floats: hi = bf16(a, b), mid = bf16((a, b) - hi).
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& mid) {
@@ -2136,7 +2167,7 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
                                   hipStream_t s) {
     if (n_seq == 0 || max_len == 0) return hipSuccess;
     const auto* base = reinterpret_cast<const unsigned long long*>(score_base);
-    dim3 grid((max_len + 255) / 256, n_seq * n_kv);
+    const dim3 grid((max_len + 255) / 256, n_seq * n_kv);
     const size_t smem = group <= kMfmaMaxGroup ? staging_bytes(staging_rows(group)) : 0;
     const uint4* ap = static_cast<const uint4*>(arena);
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
@@ -2162,12 +2193,16 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
     if ((uint64_t)nseg * k > kTopkMaxCandidates) return hipErrorInvalidValue;  // checked by the ABI
     uint32_t* cand_key = static_cast<uint32_t*>(workspace);
     uint32_t* cand_idx = cand_key + (size_t)rows * nseg * k;
-    topk_segment_kernel<<<dim3(nseg, rows), kSegThreads, 0, s>>>(scores, seq_len, base, hq, k, nseg,
+    // Rows along x: every row's first segment is dispatched before any
+    // second segment, so the workgroups of short rows that have no work in
+    // the later segments gather at the end of the grid instead of diluting
+    // the occupancy throughout.
+    topk_segment_kernel<<<dim3(rows, nseg), kSegThreads, 0, s>>>(scores, seq_len, base, hq, k, nseg,
                                                                  cand_key, cand_idx);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    topk_merge_kernel<<<rows, kTopkThreads, 0, s>>>(cand_key, cand_idx, seq_len, hq, k, nseg,
-                                                    topk_idx, topk_val);
+    topk_merge_kernel<<<rows, kMergeThreads, (size_t)nseg * k * 8, s>>>(
+        cand_key, cand_idx, seq_len, hq, k, nseg, topk_idx, topk_val);
     return hipGetLastError();
 }
 
