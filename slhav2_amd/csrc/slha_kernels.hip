@@ -746,11 +746,29 @@ __device__ __forceinline__ const uint4* tile_chunk(const uint4* region, uint32_t
     return region + 8u * u + (chunk ^ (u & 7u));
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// +-1 bytes of 8 sign bits: byte j = 1 - 2 * bit j (0x01 or 0xFF).
+__device__ __forceinline__ uint2 pm1_bytes(uint32_t b) {
+    auto spread = [](uint32_t n) {  // bit j of a nibble to bit 0 of byte j
+        return ((n * 0x00204081u) & 0x01010101u) * 0xFEu | 0x01010101u;
+    };
+    return make_uint2(spread(b & 15u), spread((b >> 4) & 15u));
+}
+
+// 16 sign bits as an i8 MFMA operand of +-1 bytes (bit j -> byte j), from
+// the 256-entry byte table.
+__device__ __forceinline__ v4i pm1_operand(uint32_t bits16, const uint2* lut) {
+    const uint2 a = lut[bits16 & 0xFFu], b = lut[(bits16 >> 8) & 0xFFu];
+    return v4i{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
+}
+
 template <int CLS>
 __device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t group,
                                                 const uint16_t* qh, const float* qexp,
-                                                const uint32_t* qsl, float* __restrict__ out,
-                                                uint32_t n_tok, uint32_t tile0) {
+                                                const uint32_t* qsl, const uint2* lut,
+                                                float* __restrict__ out, uint32_t n_tok,
+                                                uint32_t tile0) {
     const uint32_t lane = threadIdx.x & 63u, c = lane & 15u, h = lane >> 4;
     const uint32_t nrb = (group + 15u) >> 4;  // 2..4 query blocks
     uint32_t lat[4][4], gsw[4][2];
@@ -863,6 +881,21 @@ __device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t gr
             }
         }
     }
+    // Residual term on i8 MFMA: with +-1 bytes x = 1 - 2 bit, the dot product
+    // of a query's and a tile's 256 sign bits is 256 - 2 * Hamming, exactly.
+    // The i8 MFMA's K = 64 slots of lane group h are bits 64 kc + 16 h ..
+    // +15 on both operands. A (queries, rows q = 16 rb + L % 16) is expanded
+    // once per wave; B (tiles) once per tile block.
+    v4i aq[4][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const uint32_t q = 16u * rb + c;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+            const uint32_t w = (uint32_t)rb < nrb && q < group ? qsl[8u * q + 2u * kc + (h >> 1)] : 0u;
+            aq[rb][kc] = pm1_operand(w >> (16u * (h & 1u)), lut);
+        }
+    }
     // Epilogue: lane L owns tiles u = 16 cb + L % 16 and queries q = 16 rb + 4h + r.
     const float lvl = CLS == kClsInt4 ? 1.0f : 0.25f;  // TQ3 levels were scaled by 4
 #pragma unroll
@@ -876,20 +909,26 @@ __device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t gr
         const float s255 = __uint_as_float(m6.x) * (1.0f / 255.0f) * lvl;
         const float lambda = __uint_as_float(m6.y);
         const bool warm = ((m7.y >> 16) & kFlagWarm) != 0;
+        const bool odd = (h >> 1) != 0;  // word 2 kc + (h >> 1) of the residual
+        const uint32_t sh = 16u * (h & 1u);
+        v4i bt[4];
+        bt[0] = pm1_operand((odd ? r0.y : r0.x) >> sh, lut);
+        bt[1] = pm1_operand((odd ? r0.w : r0.z) >> sh, lut);
+        bt[2] = pm1_operand((odd ? r1.y : r1.x) >> sh, lut);
+        bt[3] = pm1_operand((odd ? r1.w : r1.z) >> sh, lut);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             if ((uint32_t)rb >= nrb) continue;
+            v4i dot = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc)
+                dot = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq[rb][kc], bt[kc], dot, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t q = 16u * rb + 4u * h + r;
                 if (q >= group) continue;
-                const uint4 s0 = reinterpret_cast<const uint4*>(qsl + 8u * q)[0];
-                const uint4 s1 = reinterpret_cast<const uint4*>(qsl + 8u * q)[1];
-                const uint32_t hd = __popc(r0.x ^ s0.x) + __popc(r0.y ^ s0.y) + __popc(r0.z ^ s0.z) +
-                                    __popc(r0.w ^ s0.w) + __popc(r1.x ^ s1.x) + __popc(r1.y ^ s1.y) +
-                                    __popc(r1.z ^ s1.z) + __popc(r1.w ^ s1.w);
                 float sc = acc[rb][cb][r] * (s255 * qexp[q]);
-                if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)hd, sc);
+                if (!warm) sc = fmaf(lambda, (float)dot[r], sc);  // (float)(256 - 2 ham)
                 if (t < n_tok) out[(size_t)q * n_tok + t] = sc;
             }
         }
@@ -910,8 +949,10 @@ __global__ __launch_bounds__(256) void score_rows_wide_kernel(
     const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
     __shared__ float cb[16];
     __shared__ uint4 tile_lds[4][512];
+    __shared__ uint2 pm1_lut[256];
     extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_staging_bytes(group)
     const uint32_t row = blockIdx.y;
+    pm1_lut[threadIdx.x] = pm1_bytes(threadIdx.x);
     const size_t qrow0 = (size_t)row * group;
     const uint32_t rows_alloc = staging_rows(group);
     uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
@@ -934,11 +975,11 @@ __global__ __launch_bounds__(256) void score_rows_wide_kernel(
     const int c0 = __builtin_amdgcn_readfirstlane(cls);
     const bool uniform = c0 >= 0 && __all(cls == c0 || cls < 0);
     if (uniform && c0 == kClsInt4) {
-        score_wave_wide<kClsInt4>(tile_lds[wave], group, q16, qexp, qsl, out, n_tok, wave0);
+        score_wave_wide<kClsInt4>(tile_lds[wave], group, q16, qexp, qsl, pm1_lut, out, n_tok, wave0);
         return;
     }
     if (uniform && c0 == kClsTQ3) {
-        score_wave_wide<kClsTQ3>(tile_lds[wave], group, q16, qexp, qsl, out, n_tok, wave0);
+        score_wave_wide<kClsTQ3>(tile_lds[wave], group, q16, qexp, qsl, pm1_lut, out, n_tok, wave0);
         return;
     }
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
