@@ -393,7 +393,7 @@ def run_c5(args) -> int:
          "kv_heads": n_kv, "page_tiles": page, "tiles": total_tiles, "warm_tiles": n_warm,
          "pairs": pairs, "max_len": max(lens), "min_len": min(lens), "k": k,
          "parallelism": "none (1 GPU)"},
-        roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_rows_kernel"),
+        roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_segment_kernel + topk_merge_kernel"),
         score_only_ms=ms_score, topk_ms=ms - ms_score,
         score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9)), flush=True)
     return 0
