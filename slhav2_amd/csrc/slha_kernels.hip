@@ -935,6 +935,57 @@ __device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t gr
     }
 }
 
+// Query staging of score_rows_wide_kernel in two phases, as stage_issue /
+// stage_commit: the loads of the row's queries (wave wv takes rows wv + 4k)
+// and sign words go out before the tile DMA, so waiting for them does not
+// wait for the tiles; the conversion and LDS stores come after. Buffer loads
+// past `group` rows read zero.
+constexpr uint32_t kWideRowsPerWave = kMfmaMaxGroup / 4;
+struct WideQueryRegs {
+    float v0[kWideRowsPerWave], v1[kWideRowsPerWave];
+    uint32_t sw[kMfmaMaxGroup * 8 / 256];
+};
+
+__device__ __forceinline__ void wide_stage_issue(const float* __restrict__ qc,
+                                                 const uint32_t* __restrict__ qs, size_t qrow0,
+                                                 uint32_t group, WideQueryRegs& r) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(qc + qrow0 * kDC), 0, __builtin_amdgcn_readfirstlane(group * kDC * 4u),
+        0x00020000);
+    const uint32_t voff = 4u * f16_stage_dim(lane);
+#pragma unroll
+    for (uint32_t k = 0; k < kWideRowsPerWave; ++k) {
+        const uint32_t soff = (wv + 4u * k) * kDC * 4u;
+        r.v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, voff, soff, 0));
+        r.v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, voff + 16u, soff, 0));
+    }
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(qs + qrow0 * 8), 0, __builtin_amdgcn_readfirstlane(group * 32u),
+        0x00020000);
+#pragma unroll
+    for (uint32_t k = 0; k < kMfmaMaxGroup * 8 / 256; ++k)
+        r.sw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (threadIdx.x + 256u * k), 0, 0);
+}
+
+__device__ __forceinline__ void wide_stage_commit(const WideQueryRegs& r, uint32_t group,
+                                                  uint16_t* q16, float* qexp, uint32_t* qsl) {
+    const uint32_t wv = threadIdx.x >> 6;
+    const uint32_t rows = (group + 3u) & ~3u;
+#pragma unroll
+    for (uint32_t k = 0; k < kWideRowsPerWave; ++k)
+        if (wv + 4u * k < rows) stage_f16_row(r.v0[k], r.v1[k], wv + 4u * k, q16, qexp);
+#pragma unroll
+    for (uint32_t k = 0; k < kMfmaMaxGroup * 8 / 256; ++k) {
+        const uint32_t i = threadIdx.x + 256u * k;
+        if (i < group * 8u) {
+            // inline asm store, as in stage_f16_row: no wait for the tile DMA
+            asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(qsl + i)), "v"(r.sw[k]) : "memory");
+        }
+    }
+}
+
 // Dynamic LDS of score_rows_wide_kernel: f16 hi/lo queries, their 2^e
 // factors and the queries' sign words (no f32 copy).
 __host__ __device__ constexpr size_t wide_staging_bytes(uint32_t group) {
@@ -961,11 +1012,12 @@ __global__ __launch_bounds__(256) void score_rows_wide_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    WideQueryRegs qr;
+    wide_stage_issue(qc, qs, qrow0, group, qr);
     fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
     stage_codebook(cb);
-    stage_queries_f16(qc, qrow0, group, q16, qexp);
-    for (uint32_t i = threadIdx.x; i < group * 8u; i += blockDim.x) qsl[i] = qs[qrow0 * 8 + i];
-    __syncthreads();
+    wide_stage_commit(qr, group, q16, qexp, qsl);
+    lds_barrier();
     uint32_t w[32];
     fetch_tiles_readback(tile_lds[wave], w);
     const uint32_t t = wave0 + (threadIdx.x & 63u);
