@@ -347,7 +347,8 @@ void score_host_tiles(const SciRustSlhaTile* tiles, size_t n, const float* qc, c
     check_hip(hipMemcpyAsync(td, tiles, n * sizeof(SciRustSlhaTile), hipMemcpyHostToDevice, s), "H2D tiles");
     check_hip(hipMemcpyAsync(qcd, qc, 128 * sizeof(float), hipMemcpyHostToDevice, s), "H2D q_coarse");
     check_hip(hipMemcpyAsync(qsd, qs, 4 * sizeof(uint64_t), hipMemcpyHostToDevice, s), "H2D q_sign");
-    check_hip(launch_score_rows(td, 1, (uint32_t)n, 1, qcd, qsd, true, sd, nullptr, s), "score kernel");
+    check_hip(launch_score_rows(td, 1, (uint32_t)n, 1, qcd, qsd, true, sd, nullptr, nullptr, s),
+              "score kernel");
     check_hip(hipMemcpyAsync(out, sd, n * sizeof(float), hipMemcpyDeviceToHost, s), "D2H scores");
     check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
@@ -761,9 +762,14 @@ int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n
         if (!tiles_dev || !q_coarse_dev || !q_sign_dev || !scores_dev)
             fail(SLHA_ERR_NULL, "slha_gpu_score received a NULL pointer");
         require_device();
+        const hipStream_t hs = static_cast<hipStream_t>(stream);
+        void* ws = stream_workspace(score_rows_workspace_bytes((uint32_t)n_rows, (uint32_t)group,
+                                                               mode == SLHA_SCORE_EXACT,
+                                                               hamming_dev != nullptr),
+                                    hs);
         check_hip(launch_score_rows(tiles_dev, (uint32_t)n_rows, (uint32_t)n_tok, (uint32_t)group,
                                     q_coarse_dev, q_sign_dev, mode == SLHA_SCORE_EXACT, scores_dev,
-                                    hamming_dev, static_cast<hipStream_t>(stream)),
+                                    hamming_dev, ws, hs),
                   "score kernel");
     });
 }

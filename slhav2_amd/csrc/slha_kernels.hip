@@ -991,19 +991,50 @@ __device__ __forceinline__ void wide_stage_commit(const WideQueryRegs& r, uint32
 __host__ __device__ constexpr size_t wide_staging_bytes(uint32_t group) {
     return (size_t)staging_rows(group) * (kQStrideH * 2u + 4u) + (size_t)group * 32u;
 }
+// The staging as an image in global memory, rounded up to whole 1 KiB DMA
+// blocks (one wave-wide 16-B-per-lane load each).
+__host__ __device__ constexpr size_t wide_image_bytes(uint32_t group) {
+    return (wide_staging_bytes(group) + 1023u) & ~(size_t)1023u;
+}
+
+// One workgroup per row: the row's wide staging (f16 hi/lo queries, 2^e
+// factors, sign words), built in LDS exactly as score_rows_wide_kernel reads
+// it and copied out as an image that the scoring workgroups load with DMA.
+__global__ __launch_bounds__(256) void stage_wide_image_kernel(const float* __restrict__ qc,
+                                                               const uint32_t* __restrict__ qs,
+                                                               uint32_t group,
+                                                               uint4* __restrict__ img) {
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_image_bytes(group)
+    const uint32_t row = blockIdx.x;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t rows_alloc = staging_rows(group);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
+    float* qexp = reinterpret_cast<float*>(q16 + rows_alloc * kQStrideH);
+    uint32_t* qsl = reinterpret_cast<uint32_t*>(qexp + rows_alloc);
+    const uint32_t n16 = (uint32_t)(wide_image_bytes(group) / 16);
+    uint4* l4 = reinterpret_cast<uint4*>(qlds);
+    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) l4[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    WideQueryRegs qr;
+    wide_stage_issue(qc, qs, qrow0, group, qr);
+    wide_stage_commit(qr, group, q16, qexp, qsl);
+    __syncthreads();
+    uint4* out = img + (size_t)row * n16;
+    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) out[i] = l4[i];
+}
 
 // Scoring of tile rows for 16 < group <= kMfmaMaxGroup: the coalesced tile
 // fetch of score_rows_fast_kernel; INT4 and TQ3 waves run score_wave_wide,
 // waves of other codecs the per-lane path.
 __global__ __launch_bounds__(256) void score_rows_wide_kernel(
     const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
-    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores,
+    const uint4* __restrict__ img) {
     __shared__ float cb[16];
     __shared__ uint4 tile_lds[4][512];
     __shared__ uint2 pm1_lut[256];
-    extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_staging_bytes(group)
+    extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_image_bytes(group)
     const uint32_t row = blockIdx.y;
-    pm1_lut[threadIdx.x] = pm1_bytes(threadIdx.x);
     const size_t qrow0 = (size_t)row * group;
     const uint32_t rows_alloc = staging_rows(group);
     uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
@@ -1012,12 +1043,26 @@ __global__ __launch_bounds__(256) void score_rows_wide_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
-    WideQueryRegs qr;
-    wide_stage_issue(qc, qs, qrow0, group, qr);
+    // The row's staging image (stage_wide_image_kernel) goes into LDS by
+    // DMA, 1 KiB per wave instruction, ahead of the tile DMA; each wave then
+    // waits for its image loads alone (the 8 tile loads stay in flight)
+    // before the barrier that publishes the image to the other waves.
+    {
+        const uint32_t nblk_img = (uint32_t)(wide_image_bytes(group) / 1024);
+        const uint32_t lane = threadIdx.x & 63u;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint4*>(img + (size_t)row * nblk_img * 64), 0,
+            __builtin_amdgcn_readfirstlane(nblk_img * 1024u), 0x00020000);
+        for (uint32_t b = wave; b < nblk_img; b += 4u)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(qlds) + 1024u * b),
+                16, lane * 16u, b * 1024u, 0, 0);
+    }
     fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
     stage_codebook(cb);
-    wide_stage_commit(qr, group, q16, qexp, qsl);
-    lds_barrier();
+    pm1_lut[threadIdx.x] = pm1_bytes(threadIdx.x);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    __syncthreads();
     uint32_t w[32];
     fetch_tiles_readback(tile_lds[wave], w);
     const uint32_t t = wave0 + (threadIdx.x & 63u);
@@ -2218,9 +2263,14 @@ __global__ __launch_bounds__(256) void ccos_apply_kernel(uint4* __restrict__ til
 // ---------------------------------------------------------------------------
 // Launchers
 
+size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
+    const bool wide = !exact && !ham && group > kRegStageMaxGroup && group <= kMfmaMaxGroup;
+    return wide ? (size_t)n_rows * wide_image_bytes(group) : 0;
+}
+
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
-                             uint32_t* ham, hipStream_t s) {
+                             uint32_t* ham, void* workspace, hipStream_t s) {
     if (n_rows == 0 || n_tok == 0 || group == 0) return hipSuccess;
     dim3 grid((n_tok + 255) / 256, n_rows);
     const uint4* tp = static_cast<const uint4*>(tiles);
@@ -2232,9 +2282,15 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
             score_rows_fast_kernel<4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= kRegStageMaxGroup)
             score_rows_fast_kernel<16><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
-        else
-            score_rows_wide_kernel<<<grid, 256, wide_staging_bytes(group), s>>>(tp, n_tok, group,
-                                                                              qc, qsw, scores);
+        else {
+            if (!workspace) return hipErrorInvalidValue;  // score_rows_workspace_bytes
+            uint4* img = static_cast<uint4*>(workspace);
+            stage_wide_image_kernel<<<n_rows, 256, wide_image_bytes(group), s>>>(qc, qsw, group, img);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            score_rows_wide_kernel<<<grid, 256, wide_image_bytes(group), s>>>(tp, n_tok, group, qc,
+                                                                            qsw, scores, img);
+        }
         return hipGetLastError();
     }
     if (exact) {

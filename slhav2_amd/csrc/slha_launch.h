@@ -21,9 +21,12 @@ constexpr uint32_t kMaxTopK = 256;
 constexpr uint32_t kTopkSeg = 16384;
 constexpr uint32_t kTopkMaxCandidates = 8192;
 
+// `workspace`: device memory of score_rows_workspace_bytes() (a staging image
+// per row for 16 < group <= 64 in fast mode; otherwise unused, may be null).
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
-                             uint32_t* ham, hipStream_t s);
+                             uint32_t* ham, void* workspace, hipStream_t s);
+size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham);
 hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
                                   const uint32_t* page_table, uint32_t max_pages,
                                   const uint32_t* seq_len, const uint64_t* score_base,
