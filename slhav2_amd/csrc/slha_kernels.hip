@@ -175,6 +175,15 @@ __device__ __forceinline__ void decode_group_exact(const uint32_t* w, int g, con
 // group at a time for one query at a time; the empty asm makes the tile words
 // opaque per query so the compiler cannot hoist all 128 decoded values out of
 // the query loop (which would cost 128 VGPRs and most of the occupancy).
+// Scores and Hamming distances are written once and not read again by the
+// scoring kernels: non-temporal stores stream them out of L2 as they are
+// written instead of leaving 4 B per pair dirty there. At the C2 size
+// (4 MiB of scores per launch) this took the launch from ~9.5 to ~8.9 us.
+template <typename T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 template <int CLS, bool EXACT, bool HAM>
 __device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group, size_t qrow0,
                                            const float* __restrict__ qc,
@@ -221,8 +230,8 @@ __device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group,
             else
                 score = fmaf(lambda, 256.0f - 2.0f * (float)h, score);
         }
-        out[(size_t)j * stride + t] = score;
-        if constexpr (HAM) ham[(size_t)j * stride + t] = h;
+        store_out(out + (size_t)j * stride + t, score);
+        if constexpr (HAM) store_out(ham + (size_t)j * stride + t, h);
     }
 }
 
@@ -316,7 +325,7 @@ __device__ __forceinline__ void score_wave_mfma(const uint32_t* w_in, bool valid
                 float sc = acc[rr];
                 const uint32_t h = hamming_words(w + 16, qs + (qrow0 + c0 + rr) * 8);
                 if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
-                if (valid) out[(size_t)(c0 + rr) * stride + t] = sc;
+                if (valid) store_out(out + (size_t)(c0 + rr) * stride + t, sc);
             }
         }
     }
@@ -409,7 +418,7 @@ __device__ __forceinline__ void score_wave_int4_f16(const uint32_t* w_in, bool v
                 float sc = dot[rr] * (s255 * qexp[c0 + rr]);
                 const uint32_t h = hamming_words(w + 16, qs + (qrow0 + c0 + rr) * 8);
                 if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
-                if (valid) out[(size_t)(c0 + rr) * stride + t] = sc;
+                if (valid) store_out(out + (size_t)(c0 + rr) * stride + t, sc);
             }
         }
         if constexpr (ONE_CHUNK) break;
@@ -929,7 +938,7 @@ __device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t gr
                 if (q >= group) continue;
                 float sc = acc[rb][cb][r] * (s255 * qexp[q]);
                 if (!warm) sc = fmaf(lambda, (float)dot[r], sc);  // (float)(256 - 2 ham)
-                if (t < n_tok) out[(size_t)q * n_tok + t] = sc;
+                if (t < n_tok) store_out(out + (size_t)q * n_tok + t, sc);
             }
         }
     }
