@@ -41,18 +41,22 @@ ROTATION = 10
 PEAK_HBM_GBS = 8000.0
 TILE_BYTES = 128
 SCORE_KERNEL = "slha::score_rows_fast_kernel<4u>"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "score_rows_fast_kernel_c2_traffic.txt"
+PROFILES = ROOT / "profiles"
 COPY_BYTES = 1 << 30
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per score launch from the committed counter summary, if any."""
-    try:
-        for line in TRAFFIC_SUMMARY.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
-    except (OSError, ValueError):
-        pass
+def measured_traffic(label: str) -> int | None:
+    """Calibrated HBM bytes per step of workload `label` (c2, c3_nf4, c3_mx_int4,
+    c4, c5) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summaries in
+    profiles/ (line "traffic_bytes_per_launch[<label>]: N"), if present."""
+    key = f"traffic_bytes_per_launch[{label}]:"
+    for path in sorted(PROFILES.glob("*.txt")):
+        try:
+            for line in path.read_text().splitlines():
+                if line.startswith(key):
+                    return int(line.split(":", 1)[1])
+        except (OSError, ValueError):
+            continue
     return None
 
 
@@ -212,10 +216,10 @@ def line(metric, value, unit, steps, warmup, ms, dtype, config, **extra) -> dict
     return out
 
 
-def hbm_roofline(nbytes: float, ms: float, kernel: str) -> dict:
+def hbm_roofline(nbytes: float, ms: float, kernel: str, label: str) -> dict:
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": gbs / PEAK_HBM_GBS, "traffic": None, "kernel": kernel,
+            "frac": gbs / PEAK_HBM_GBS, "traffic": measured_traffic(label), "kernel": kernel,
             "algorithmic_bytes_per_launch": nbytes, "kernel_ms": ms}
 
 
@@ -265,7 +269,7 @@ def run_c3(args) -> int:
             ex = s.gpu_score(tiles[:1], qc[:GROUP], qs[:GROUP], group=GROUP, mode=s.SCORE_EXACT)
             err = ((scores[:GROUP] - ex).abs() / (1 + ex.abs())).max().item()
             results[name] = {"ms_per_step": ms, "tiles_per_s": n_q * n_tok / (ms * 1e-3),
-                             "roofline": hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<4u>"),
+                             "roofline": hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<4u>", f"c3_{name}"),
                              "encode_keys_per_s": rows * n_tok / (enc_ms * 1e-3),
                              "encode_ms": enc_ms, "fast_vs_exact_max_rel_err_row0": err}
     best = results["mx_int4"]
@@ -315,7 +319,7 @@ def run_c4(args) -> int:
         "tiles/s", steps, warmup, ms, "f32",
         {"workload": "C4 bulk encode + score, TQ3 + RHT (BASELINE configs[3])", "keys": n_keys,
          "queries": n_q, "codec": "tq3", "rht": True, "parallelism": "none (1 GPU)"},
-        roofline=hbm_roofline(nbytes, ms, "slha::score_rows_wide_kernel"),
+        roofline=hbm_roofline(nbytes, ms, "slha::score_rows_wide_kernel", "c4"),
         score_tflops=flops / (ms * 1e-3) / 1e12, fast_vs_exact_max_rel_err_first4096=err,
         encode={"keys_per_s": n_keys / (enc_ms * 1e-3), "ms": enc_ms,
                 "hbm_gbs": enc_bytes / (enc_ms * 1e-3) / 1e9,
@@ -393,7 +397,7 @@ def run_c5(args) -> int:
          "kv_heads": n_kv, "page_tiles": page, "tiles": total_tiles, "warm_tiles": n_warm,
          "pairs": pairs, "max_len": max(lens), "min_len": min(lens), "k": k,
          "parallelism": "none (1 GPU)"},
-        roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_segment_kernel + topk_merge_kernel"),
+        roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_segment_kernel + topk_merge_kernel", "c5"),
         score_only_ms=ms_score, topk_ms=ms - ms_score,
         score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9)), flush=True)
     return 0
@@ -520,7 +524,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic("c2"),
             "kernel": SCORE_KERNEL,
             "algorithmic_bytes_per_launch": nbytes,
             "kernel_ms": kern_ms,

@@ -634,6 +634,10 @@ __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group
 // hold the data in flight. The buffer's range ends at the last valid tile:
 // slots of tiles at or past n_valid read as zero. The compiler waits for
 // these loads (vmcnt) before the region is read back.
+// Cache policy of the tile loads: nt (streaming). A launch reads each tile
+// once; at C2 this took the launch from ~8.9 to ~8.7 us.
+constexpr int kCachePolicyNT = 2;
+
 __device__ __forceinline__ void fetch_tiles_lds(const uint4* wave_base, uint32_t n_valid,
                                                 uint4* region) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -647,7 +651,7 @@ __device__ __forceinline__ void fetch_tiles_lds(const uint4* wave_base, uint32_t
     for (int j = 0; j < 8; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rsrc, (__attribute__((address_space(3))) void*)(region + 64 * j), 16, in_tile * 16u,
-            1024 * j, 0, 0);
+            1024 * j, 0, kCachePolicyNT);
 }
 
 // Lane l reads tile l back from a region filled by fetch_tiles_lds; the XOR
