@@ -141,7 +141,10 @@ int32_t slha_score_tiles(const SlhaModel* model, const SciRustSlhaTile* tiles, s
 char* slha_audit(void);
 void slha_free_string(char* string);
 
-/* slha.h:219,225 — projection models. */
+/* slha.h:219,225 — projection models. slha_weights_load reads a .slhw v1/v2
+ * learned projection (d > 128; scirust/src/weights.rs:8-31, 159-311) with the
+ * reference's checks; its GPU kernels hold next_pow2(d) (with RHT, else d)
+ * <= 16384 dimensions, and larger models are rejected with a message. */
 SlhaModel* slha_weights_load(const char* path);
 size_t slha_model_dim(const SlhaModel* model);
 

@@ -43,25 +43,36 @@ extern "C" {
  */
 SlhaModel* slha_model_new_raw128(uint64_t seed, int32_t rht, int32_t residual_mode);
 
-/* Copy the model's Z (256*128 floats, row-major) and RHT diagonal (128
- * floats, may be NULL; all +1 when the model has no RHT) to host memory. */
+/* Copy the model's Z (256 x d_pad floats, row-major) and RHT diagonal (d_pad
+ * floats, may be NULL; all +1 when the model has no RHT) to host memory.
+ * d_pad = slha_model_pad_dim(model): 128 for head_dim-128 models; for a
+ * learned model next_pow2(d) with RHT, else d (learned.rs:233-245). */
 int32_t slha_model_projection(const SlhaModel* model, float* z_out, float* rht_diag_out);
+size_t slha_model_pad_dim(const SlhaModel* model);
+
+/* Copy the latent projection P (128 x d floats, row-major) to host memory:
+ * the .slhw payload of a learned model, the identity for head_dim 128. */
+int32_t slha_model_latent_projection(const SlhaModel* model, float* p_out);
 
 /*
- * Encode keys[n_rows][n_tok][128] (f32 or bf16, device) into
- * tiles_dev[n_rows][n_tok]. Row r gets head_id = r % n_kv_heads, token t gets
- * token_id = position = pos0 + t. warm != 0 sets FLAG_WARM. Bit-identical to
- * the oracle's mode R / mode Z encode (codes, residual bits, sigma, lambda).
- * Replaces slha_encode_key (slha-c/src/lib.rs:708-752) for batches.
+ * Encode keys[n_rows][n_tok][d] (f32 or bf16, device; d = slha_model_dim)
+ * into tiles_dev[n_rows][n_tok]. Row r gets head_id = r % n_kv_heads, token t
+ * gets token_id = position = pos0 + t. warm != 0 sets FLAG_WARM. Bit-identical
+ * to the oracle's encode: mode R / mode Z for head_dim-128 models,
+ * LearnedModel::encode_with (learned.rs:353-408) for learned models (codes,
+ * residual bits, sigma, lambda). Replaces slha_encode_key
+ * (slha-c/src/lib.rs:708-752) for batches.
  */
 int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t key_dtype,
                         size_t n_rows, size_t n_tok, size_t n_kv_heads, uint32_t pos0,
                         int32_t codec, int32_t warm, SciRustSlhaTile* tiles_dev, void* stream);
 
 /*
- * Prepare n_q queries: q_coarse_dev[n_q][128] = q (identity latent) and
- * q_sign_dev[n_q][4] = sign bits of Z*RHT(q). Replaces slha_prepare_query
- * (slha-c/src/lib.rs:420-463) for batches.
+ * Prepare n_q queries q_dev[n_q][d]: q_coarse_dev[n_q][128] = P q (the query
+ * itself for head_dim-128 models; LearnedModel::query_coarse,
+ * learned.rs:267-273, for learned ones) and q_sign_dev[n_q][4] = sign bits
+ * of Z*RHT(q). Replaces slha_prepare_query (slha-c/src/lib.rs:420-463) for
+ * batches.
  */
 int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int32_t q_dtype,
                                  size_t n_q, float* q_coarse_dev, uint64_t* q_sign_dev,
@@ -94,7 +105,8 @@ int32_t slha_gpu_validate_tiles(const SciRustSlhaTile* tiles_dev, size_t n, uint
                                 void* stream);
 
 /*
- * Decode tiles to floats: out_dev[n][128] = dequant_latent (tile.rs:249-255);
+ * Decode tiles to floats: out_dev[n][d] = reconstruct(dequant_latent)
+ * (tile.rs:249-255, learned.rs:276-286; the identity for head_dim-128 models);
  * with_residual != 0 adds the sign-sketch residual estimate of
  * LearnedModel::reconstruct_from_tile (learned.rs:288-320) when the model has
  * no RHT.

@@ -467,6 +467,88 @@ void orc_query_sign(const float* q, const float* z, const float* rht_diag, uint6
     orc_sign_bits(z, ORC_D_C, buf, out);
 }
 
+/* ---- learned.rs (d > 128, projection loaded from .slhw: scale_k = 1) ---- */
+
+static float orc_evec_dot(const float* p, size_t d, int k, const float* v) { /* :257-265 */
+    const float* row = p + (size_t)k * d;
+    float acc = 0.0f;
+    for (size_t i = 0; i < d; ++i) acc += row[i] * v[i];
+    return acc;
+}
+
+void orc_learned_latent(const float* p, size_t d, const float* key, float* h) { /* :267-273 latent */
+    for (int k = 0; k < ORC_D_C; ++k) h[k] = orc_evec_dot(p, d, k, key) / 1.0f;
+}
+
+void orc_learned_query_coarse(const float* p, size_t d, const float* q, float* out) { /* :267-273 */
+    for (int k = 0; k < ORC_D_C; ++k) out[k] = orc_evec_dot(p, d, k, q) * 1.0f;
+}
+
+void orc_learned_reconstruct(const float* p, size_t d, const float* h, float* out) { /* :276-286 */
+    for (size_t i = 0; i < d; ++i) out[i] = 0.0f;
+    for (int k = 0; k < ORC_D_C; ++k) {
+        const float w = h[k] * 1.0f;
+        const float* row = p + (size_t)k * d;
+        for (size_t i = 0; i < d; ++i) out[i] += w * row[i];
+    }
+}
+
+/* sign_bits (:326-347): Z [256][d_pad] against RHT(v) or v itself. */
+static void orc_learned_sign_bits(const float* z, const float* diag, size_t d, size_t d_pad,
+                                  const float* v, uint64_t* out) {
+    float* buf = (float*)malloc(d_pad * sizeof(float));
+    if (diag)
+        orc_rht_transform(diag, d, d_pad, v, buf);
+    else
+        memcpy(buf, v, d * sizeof(float));
+    orc_sign_bits(z, d_pad, buf, out);
+    free(buf);
+}
+
+void orc_learned_query(const float* p, const float* z, const float* diag, size_t d, size_t d_pad,
+                       const float* q, float* q_coarse, uint64_t* q_sign) {
+    orc_learned_query_coarse(p, d, q, q_coarse);
+    orc_learned_sign_bits(z, diag, d, d_pad, q, q_sign);
+}
+
+int orc_learned_encode(const float* p, const float* z, const float* diag, size_t d, size_t d_pad,
+                       const float* key, uint32_t position, int codec, int warm,
+                       orc_tile* out) { /* encode_with, :353-408 */
+    float h[ORC_D_C];
+    orc_learned_latent(p, d, key, h);
+    orc_tile t;
+    /* codes, scale, gs and flags as the head_dim-128 encoder, mode Z */
+    int rc = orc_encode_key(h, codec, ORC_RESIDUAL_Z, NULL, NULL, position, 0, warm, &t);
+    if (rc) return rc;
+    float* recon = (float*)malloc(d * sizeof(float));
+    float* e = (float*)malloc(d * sizeof(float));
+    orc_learned_reconstruct(p, d, h, recon); /* residual from the un-quantised latent */
+    for (size_t i = 0; i < d; ++i) e[i] = key[i] - recon[i];
+    orc_learned_sign_bits(z, diag, d, d_pad, e, t.residual_bitmap);
+    float acc = 0.0f; /* sum::<f32>() of e_i * e_i, then / d, sqrt (f32) */
+    for (size_t i = 0; i < d; ++i) acc += e[i] * e[i];
+    t.residual_sigma = sqrtf(acc / (float)d);
+    t.dynamic_lambda = t.residual_sigma * orc_analytic_lambda_c();
+    free(recon);
+    free(e);
+    *out = t;
+    return 0;
+}
+
+void orc_learned_decode(const float* p, const float* z, size_t d, size_t d_pad, int has_rht,
+                        const orc_tile* t, int with_residual, float* out) { /* :276-320 */
+    float h[ORC_D_C];
+    orc_dequant_latent(t, h);
+    orc_learned_reconstruct(p, d, h, out);
+    if (!with_residual || has_rht) return;
+    const float scale = t->residual_sigma * sqrtf(3.14159265358979323846f / 2.0f) / (float)ORC_D_S;
+    for (int s = 0; s < ORC_D_S; ++s) {
+        const float sign = ((t->residual_bitmap[s >> 6] >> (s & 63)) & 1) ? -1.0f : 1.0f;
+        const float* row = z + (size_t)s * d_pad;
+        for (size_t i = 0; i < d; ++i) out[i] += sign * scale * row[i];
+    }
+}
+
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out) {
     for (size_t i = 0; i < n; ++i) {

@@ -109,6 +109,19 @@ int orc_encode_key(const float* key, int codec, int residual_mode, const float* 
                    orc_tile* out);
 void orc_query_sign(const float* q, const float* z, const float* rht_diag, uint64_t* out);
 
+/* learned.rs:257-408 — LearnedModel with a loaded projection (d > 128):
+ * P [128][d] row-major, per-component scale 1, Z [256][d_pad], RHT diagonal
+ * [d_pad] or NULL. orc_learned_encode returns 0 or a negative status. */
+void orc_learned_latent(const float* p, size_t d, const float* key, float* h);
+void orc_learned_query_coarse(const float* p, size_t d, const float* q, float* out);
+void orc_learned_reconstruct(const float* p, size_t d, const float* h, float* out);
+void orc_learned_query(const float* p, const float* z, const float* diag, size_t d, size_t d_pad,
+                       const float* q, float* q_coarse, uint64_t* q_sign);
+int orc_learned_encode(const float* p, const float* z, const float* diag, size_t d, size_t d_pad,
+                       const float* key, uint32_t position, int codec, int warm, orc_tile* out);
+void orc_learned_decode(const float* p, const float* z, size_t d, size_t d_pad, int has_rht,
+                        const orc_tile* t, int with_residual, float* out);
+
 /* Batched helpers for tests (row-major inputs, one tile per key). */
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out);

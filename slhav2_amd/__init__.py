@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 from pathlib import Path
 
 import numpy as np
@@ -111,6 +112,8 @@ _SIGS = {
     "slha_weights_free": (None, [_P]),
     "slha_model_new_raw128": (_P, [_U64, _I32, _I32]),
     "slha_model_projection": (_I32, [_P, _P, _P]),
+    "slha_model_pad_dim": (_SZ, [_P]),
+    "slha_model_latent_projection": (_I32, [_P, _P]),
     "slha_gpu_encode": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _U32, _I32, _I32, _P, _P]),
     "slha_gpu_prepare_queries": (_I32, [_P, _P, _I32, _SZ, _P, _P, _P]),
     "slha_gpu_score": (_I32, [_P, _SZ, _SZ, _P, _P, _SZ, _I32, _P, _P, _P]),
@@ -164,7 +167,9 @@ def audit() -> str:
 
 
 class Model:
-    """Head_dim-128 projection model (slha_model_new_raw128)."""
+    """A projection model: head_dim 128 (slha_model_new_raw128) or, with
+    Model.load, a learned d > 128 projection from a .slhw file
+    (slha_weights_load)."""
 
     def __init__(self, seed: int = 0, rht: bool = False, residual_mode: int = RESIDUAL_R):
         h = lib.slha_model_new_raw128(_U64(seed & (2**64 - 1)), int(bool(rht)), residual_mode)
@@ -173,6 +178,17 @@ class Model:
         self.handle = h
         self.seed, self.rht, self.residual_mode = seed, bool(rht), residual_mode
 
+    @classmethod
+    def load(cls, path) -> "Model":
+        """Learned model from a .slhw v1/v2 file (weights.rs:159-311)."""
+        h = lib.slha_weights_load(os.fsencode(path))
+        if not h:
+            raise SlhaError(ERR_IO, last_error())
+        m = cls.__new__(cls)
+        m.handle = h
+        m.seed, m.rht, m.residual_mode = None, None, None
+        return m
+
     @property
     def dim(self) -> int:
         d = lib.slha_model_dim(self.handle)
@@ -180,11 +196,26 @@ class Model:
             raise SlhaError(ERR_INVALID_HANDLE, last_error())
         return int(d)
 
+    @property
+    def pad_dim(self) -> int:
+        d = lib.slha_model_pad_dim(self.handle)
+        if d == 0:
+            raise SlhaError(ERR_INVALID_HANDLE, last_error())
+        return int(d)
+
     def projection(self) -> tuple[np.ndarray, np.ndarray]:
-        z = np.empty((256, 128), np.float32)
-        diag = np.empty(128, np.float32)
+        """(Z [256, d_pad], RHT diagonal [d_pad]; all +1 without RHT)."""
+        dp = self.pad_dim
+        z = np.empty((256, dp), np.float32)
+        diag = np.empty(dp, np.float32)
         _check(lib.slha_model_projection(self.handle, _ptr(z), _ptr(diag)))
         return z, diag
+
+    def latent_projection(self) -> np.ndarray:
+        """P [128, d] (the identity for head_dim 128)."""
+        p = np.empty((128, self.dim), np.float32)
+        _check(lib.slha_model_latent_projection(self.handle, _ptr(p)))
+        return p
 
     def release(self) -> None:
         if self.handle:
@@ -249,16 +280,50 @@ def encode_key(model: Model, key, position: int, codec: int) -> np.ndarray:
 
 def decode_latent(model: Model, tile) -> np.ndarray:
     t = _tiles_in(tile)
-    out = np.zeros(128, np.float32)
-    _check(lib.slha_decode_latent(model.handle, _ptr(t), _ptr(out), 128))
+    d = model.dim
+    out = np.zeros(d, np.float32)
+    _check(lib.slha_decode_latent(model.handle, _ptr(t), _ptr(out), d))
     return out
 
 
 def decode_key(model: Model, tile) -> np.ndarray:
     t = _tiles_in(tile)
-    out = np.zeros(128, np.float32)
-    _check(lib.slha_decode_key(model.handle, _ptr(t), _ptr(out), 128))
+    d = model.dim
+    out = np.zeros(d, np.float32)
+    _check(lib.slha_decode_key(model.handle, _ptr(t), _ptr(out), d))
     return out
+
+
+SLHW_MAGIC = 0x534C4857
+
+
+def _fnv1a(data: bytes) -> int:
+    h = 0x811C9DC5
+    for b in data:
+        h = ((h ^ b) * 0x01000193) & 0xFFFFFFFF
+    return h
+
+
+def slhw_bytes(p, seed: int, rht: bool, version: int = 2) -> bytes:
+    """A .slhw file image of projection p [128, d] (weights.rs:8-31, 86-141):
+    version 2 carries the FNV-1a checksum of header and payload."""
+    p = np.ascontiguousarray(p, np.float32)
+    if p.ndim != 2 or p.shape[0] != 128 or p.shape[1] <= 128:
+        raise ValueError("projection must be [128, d] with d > 128")
+    if not np.isfinite(p).all():
+        raise ValueError("projection must be finite")
+    header = struct.pack("<IIIQB3x", SLHW_MAGIC, version, p.shape[1], seed & (2**64 - 1),
+                         int(bool(rht)))
+    payload = p.astype("<f4").tobytes()
+    if version == 1:
+        return header + payload
+    return header + struct.pack("<I", _fnv1a(header + payload)) + payload
+
+
+def save_weights(path, p, seed: int, rht: bool) -> None:
+    """Write a version-2 .slhw file (weights::save, weights.rs:275-281)."""
+    with open(path, "wb") as f:
+        f.write(slhw_bytes(p, seed, rht))
 
 
 # --------------------------------------------------------------------------
@@ -288,8 +353,8 @@ def gpu_encode(model: Model, keys, codec: int, n_kv_heads: int = 1, pos0: int = 
 
     k = keys if keys.dim() == 3 else keys.unsqueeze(0)
     n_rows, n_tok, d = k.shape
-    if d != 128:
-        raise ValueError("keys must have 128 features")
+    if d != model.dim:
+        raise ValueError(f"keys must have {model.dim} features")
     dtype = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}[k.dtype]
     if out is None:
         out = torch.empty((n_rows, n_tok, 128), dtype=torch.uint8, device=k.device)
@@ -299,10 +364,10 @@ def gpu_encode(model: Model, keys, codec: int, n_kv_heads: int = 1, pos0: int = 
 
 
 def gpu_prepare_queries(model: Model, q, stream=None):
-    """q: [n, 128] f32/bf16 -> (q_coarse f32 [n,128], q_sign int64 [n,4] (u64 bits))."""
+    """q: [n, d] f32/bf16 -> (q_coarse f32 [n,128], q_sign int64 [n,4] (u64 bits))."""
     import torch
 
-    qq = q.reshape(-1, 128)
+    qq = q.reshape(-1, model.dim)
     dtype = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}[qq.dtype]
     qc = torch.empty((qq.shape[0], 128), dtype=torch.float32, device=qq.device)
     qs = torch.empty((qq.shape[0], 4), dtype=torch.int64, device=qq.device)
@@ -345,7 +410,7 @@ def gpu_decode(model: Model, tiles, with_residual: bool = False, stream=None):
     import torch
 
     t = tiles.reshape(-1, 128)
-    out = torch.empty((t.shape[0], 128), dtype=torch.float32, device=t.device)
+    out = torch.empty((t.shape[0], model.dim), dtype=torch.float32, device=t.device)
     _check(lib.slha_gpu_decode(model.handle, _dev_ptr(t), t.shape[0], int(bool(with_residual)),
                                _dev_ptr(out), _stream(stream)))
     return out

@@ -11,6 +11,9 @@
 // through per-thread device memory on a per-thread stream.
 #include <hip/hip_runtime.h>
 
+#include <sys/stat.h>
+
+#include <cerrno>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -120,19 +123,25 @@ float sqrt_half_pi() { return std::sqrt(kPi / 2.0f); }          // learned.rs:30
 
 // Device copies of a model's projection on one device.
 struct DeviceProjection {
-    const float* z = nullptr;     // [256][128] f32
-    const float* diag = nullptr;  // [128] +-1, or null without RHT
-    const void* zpack = nullptr;  // kZPackBytes, MFMA operand pack of Z
+    const float* z = nullptr;     // [256][d_pad] f32
+    const float* diag = nullptr;  // [d_pad] +-1, or null without RHT
+    const void* zpack = nullptr;  // head_dim-128 models: kZPackBytes, MFMA operand pack of Z
     float cert_scale = 0.0f;      // build_projection_pack's scale
+    const float* p = nullptr;     // learned models: [128][d]
 };
 
+// A head_dim-128 model (d = d_pad = 128, identity latent, Z [256][128]) or a
+// learned model loaded from a .slhw file (d > 128, P [128][d], Z [256][d_pad]).
 struct Model {
     size_t d = 128;
+    size_t d_pad = 128;
+    bool learned = false;
     uint64_t seed = 0;
     bool rht = false;
     int residual_mode = kResidualR;
-    std::vector<float> z;     // [256][128]
-    std::vector<float> diag;  // [128], +-1
+    std::vector<float> p;     // learned: [128][d]
+    std::vector<float> z;     // [256][d_pad]
+    std::vector<float> diag;  // [d_pad], +-1
     std::mutex mu;
     std::unordered_map<int, std::pair<DeviceProjection, void*>> dev;  // (views, allocation)
 
@@ -154,24 +163,152 @@ struct Model {
         std::lock_guard<std::mutex> lock(mu);
         auto it = dev.find(device);
         if (it == dev.end()) {
-            const size_t zb = z.size() * sizeof(float);
-            std::vector<char> host(zb + kZPackBytes + 128 * sizeof(float));
-            std::memcpy(host.data(), z.data(), zb);
-            DeviceProjection p;
-            p.cert_scale = build_projection_pack(z.data(), host.data() + zb);
-            if (rht) std::memcpy(host.data() + zb + kZPackBytes, diag.data(), 128 * sizeof(float));
+            // [Z][Z pack (head_dim-128 only)][diag][P (learned only)], 256-B aligned parts
+            const size_t zb = align_up(z.size() * sizeof(float));
+            const size_t pkb = learned ? 0 : kZPackBytes;
+            const size_t db = align_up(d_pad * sizeof(float));
+            const size_t pb = align_up(p.size() * sizeof(float));
+            std::vector<char> host(zb + pkb + db + pb, 0);
+            std::memcpy(host.data(), z.data(), z.size() * sizeof(float));
+            DeviceProjection dp;
+            if (!learned) dp.cert_scale = build_projection_pack(z.data(), host.data() + zb);
+            if (rht) std::memcpy(host.data() + zb + pkb, diag.data(), d_pad * sizeof(float));
+            if (learned) std::memcpy(host.data() + zb + pkb + db, p.data(), p.size() * sizeof(float));
             char* buf = nullptr;
             check_hip(hipMalloc(&buf, host.size()), "hipMalloc(projection)");
             check_hip(hipMemcpy(buf, host.data(), host.size(), hipMemcpyHostToDevice),
                       "hipMemcpy(projection)");
-            p.z = reinterpret_cast<const float*>(buf);
-            p.zpack = buf + zb;
-            p.diag = rht ? reinterpret_cast<const float*>(buf + zb + kZPackBytes) : nullptr;
-            it = dev.emplace(device, std::make_pair(p, static_cast<void*>(buf))).first;
+            dp.z = reinterpret_cast<const float*>(buf);
+            dp.zpack = learned ? nullptr : buf + zb;
+            dp.diag = rht ? reinterpret_cast<const float*>(buf + zb + pkb) : nullptr;
+            dp.p = learned ? reinterpret_cast<const float*>(buf + zb + pkb + db) : nullptr;
+            it = dev.emplace(device, std::make_pair(dp, static_cast<void*>(buf))).first;
         }
         return it->second.first;
     }
+
+    // Device view of a learned model for the learned_* kernels.
+    LearnedProjection learned_projection() {
+        const DeviceProjection dp = device_buffers();
+        LearnedProjection lp;
+        lp.p = dp.p;
+        lp.z = dp.z;
+        lp.diag = dp.diag;
+        lp.d = (uint32_t)d;
+        lp.d_pad = (uint32_t)d_pad;
+        lp.rht_inv = 1.0f / std::sqrt((float)d_pad);  // (n as f32).sqrt().recip(), incoherence.rs:66
+        return lp;
+    }
+
+    static size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 };
+
+// ---------------------------------------------------------------------------
+// .slhw projection files (scirust/src/weights.rs:8-31): little-endian
+//   v1: magic "SLHW" u32, version u32 = 1, d u32, seed u64, rht u8, 3 zero bytes,
+//       f32 P[128][d]
+//   v2: the same 24-byte header, then u32 FNV-1a of (header, payload), then P.
+// Checks and messages follow weights.rs:159-270 (from_bytes) and :292-311 (load).
+
+constexpr uint32_t kSlhwMagic = 0x534C4857u;        // "SLHW"
+constexpr size_t kSlhwCommonHeader = 24;
+constexpr size_t kSlhwHeaderV2 = 28;
+constexpr uint64_t kSlhwMaxBytes = 256ull << 20;   // weights.rs:289
+
+uint32_t fnv1a(const uint8_t* a, size_t na, const uint8_t* b, size_t nb) {  // weights.rs:68-81
+    uint32_t h = 0x811C9DC5u;
+    for (size_t i = 0; i < na; ++i) h = (h ^ a[i]) * 0x01000193u;
+    for (size_t i = 0; i < nb; ++i) h = (h ^ b[i]) * 0x01000193u;
+    return h;
+}
+
+uint32_t le32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+size_t next_pow2(size_t n) {  // incoherence.rs:29-35
+    size_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+std::shared_ptr<Model> parse_slhw(const std::vector<uint8_t>& bytes) {
+    const size_t n = bytes.size();
+    if (n < kSlhwCommonHeader) fail(SLHA_ERR_IO, "weights: truncated header");
+    const uint8_t* b = bytes.data();
+    if (le32(b) != kSlhwMagic) fail(SLHA_ERR_IO, "weights: bad magic (not an SLHW file)");
+    const uint32_t version = le32(b + 4);
+    if (version != 1 && version != 2)
+        fail(SLHA_ERR_IO, "weights: unsupported version %u (supported: 1 and 2)", version);
+    const size_t header = version == 1 ? kSlhwCommonHeader : kSlhwHeaderV2;
+    if (n < header) fail(SLHA_ERR_IO, "weights: truncated header");
+    const uint32_t d = le32(b + 8);
+    if (d <= 128) fail(SLHA_ERR_IO, "weights: invalid dimension %u (must be greater than D_C=128)", d);
+    uint64_t seed = 0;
+    for (int i = 7; i >= 0; --i) seed = (seed << 8) | b[12 + i];
+    if (b[20] > 1) fail(SLHA_ERR_IO, "weights: invalid RHT flag %u (expected 0 or 1)", (unsigned)b[20]);
+    const bool rht = b[20] == 1;
+    if (b[21] || b[22] || b[23]) fail(SLHA_ERR_IO, "weights: non-zero reserved header bytes");
+    const uint64_t expected = (uint64_t)header + (uint64_t)128 * d * 4;
+    if (n != expected)
+        fail(SLHA_ERR_IO, "weights: size mismatch (got %zu, expected %llu)", n,
+             (unsigned long long)expected);
+    if (version == 2) {
+        const uint32_t stored = le32(b + kSlhwCommonHeader);
+        const uint32_t calc = fnv1a(b, kSlhwCommonHeader, b + header, n - header);
+        if (stored != calc)
+            fail(SLHA_ERR_IO, "weights: checksum mismatch (stored 0x%08x, calculated 0x%08x)",
+                 stored, calc);
+    }
+    auto m = std::make_shared<Model>();
+    m->learned = true;
+    m->d = d;
+    m->seed = seed;
+    m->rht = rht;
+    m->p.resize((size_t)128 * d);
+    for (size_t i = 0; i < m->p.size(); ++i) {
+        const uint32_t u = le32(b + header + 4 * i);
+        float v;
+        std::memcpy(&v, &u, 4);
+        if (!std::isfinite(v))
+            fail(SLHA_ERR_IO, "weights: non-finite projection value at index %zu", i);
+        m->p[i] = v;
+    }
+    // LearnedModel::try_from_projection_with (learned.rs:218-250): d_pad,
+    // RHT diagonal from seed ^ 0xA2A2..A2, then Z [256][d_pad] from seed.
+    m->d_pad = rht ? next_pow2(d) : d;
+    if (m->d_pad > kLearnedMaxDPad)
+        fail(SLHA_ERR_IO,
+             "weights: d = %u (padded %zu) exceeds this build's GPU limit of %u padded dimensions",
+             d, m->d_pad, kLearnedMaxDPad);
+    m->diag.assign(m->d_pad, 1.0f);
+    if (rht) {
+        Rng r(seed ^ 0xA2A2A2A2A2A2A2A2ull);
+        for (auto& x : m->diag) x = r.next_unit() < 0.5f ? -1.0f : 1.0f;
+    }
+    m->z.resize((size_t)256 * m->d_pad);
+    Rng r(seed);
+    for (auto& x : m->z) x = r.next_gaussian();
+    return m;
+}
+
+std::shared_ptr<Model> load_slhw(const char* path) {  // weights.rs:292-311
+    struct stat st;
+    if (::stat(path, &st) != 0)
+        fail(SLHA_ERR_IO, "weights: cannot stat %s: %s", path, std::strerror(errno));
+    if (!S_ISREG(st.st_mode))
+        fail(SLHA_ERR_IO, "weights: %s is not a regular file (refusing to read a FIFO/device)", path);
+    if ((uint64_t)st.st_size > kSlhwMaxBytes)
+        fail(SLHA_ERR_IO, "weights: %s is %llu bytes, above the %llu-byte safety cap", path,
+             (unsigned long long)st.st_size, (unsigned long long)kSlhwMaxBytes);
+    std::FILE* f = std::fopen(path, "rb");
+    if (!f) fail(SLHA_ERR_IO, "weights: cannot read %s: %s", path, std::strerror(errno));
+    std::vector<uint8_t> bytes((size_t)st.st_size);
+    const size_t got = bytes.empty() ? 0 : std::fread(bytes.data(), 1, bytes.size(), f);
+    std::fclose(f);
+    if (got != bytes.size()) fail(SLHA_ERR_IO, "weights: cannot read %s: short read", path);
+    return parse_slhw(bytes);
+}
 
 }  // namespace
 
@@ -422,15 +559,21 @@ int32_t slha_prepare_query(const SlhaModel* model, const float* q, size_t d, flo
         std::vector<float> qv(d);
         std::memcpy(qv.data(), q, d * sizeof(float));
         validate_finite(qv.data(), d, "q");
-        auto zb = m->device_buffers();
         hipStream_t s;
-        char* base = staging(align256(512) + align256(512) + align256(32), &s);
+        const size_t qb = align256(d * sizeof(float));
+        char* base = staging(qb + align256(512) + align256(32), &s);
         float* qd = reinterpret_cast<float*>(base);
-        float* qcd = reinterpret_cast<float*>(base + 512);
-        uint64_t* qsd = reinterpret_cast<uint64_t*>(base + 1024);
-        check_hip(hipMemcpyAsync(qd, qv.data(), 512, hipMemcpyHostToDevice, s), "H2D q");
-        check_hip(launch_prepare_queries(qd, kDtypeF32, 1, zb.z, zb.diag, rht_inv(), qcd, qsd, s),
-                  "prepare kernel");
+        float* qcd = reinterpret_cast<float*>(base + qb);
+        uint64_t* qsd = reinterpret_cast<uint64_t*>(base + qb + 512);
+        check_hip(hipMemcpyAsync(qd, qv.data(), d * sizeof(float), hipMemcpyHostToDevice, s), "H2D q");
+        if (m->learned) {
+            check_hip(launch_learned_prepare(qd, kDtypeF32, 1, m->learned_projection(), qcd, qsd, s),
+                      "learned prepare kernel");
+        } else {
+            auto zb = m->device_buffers();
+            check_hip(launch_prepare_queries(qd, kDtypeF32, 1, zb.z, zb.diag, rht_inv(), qcd, qsd, s),
+                      "prepare kernel");
+        }
         float qc[128];
         uint64_t qs[4];
         check_hip(hipMemcpyAsync(qc, qcd, sizeof qc, hipMemcpyDeviceToHost, s), "D2H q_coarse");
@@ -573,10 +716,9 @@ SlhaModel* slha_weights_load(const char* path) {
                 return nullptr;
             }
     }
-    set_error(std::string("cannot load '") + path +
-              "': .slhw learned projections (d > 128) are not supported by this build; "
-              "use slha_model_new_raw128 for head_dim-128 keys");
-    return nullptr;
+    SlhaModel* out = nullptr;
+    const int32_t rc = ffi_status([&] { out = register_model(load_slhw(path)); });
+    return rc == SLHA_OK ? out : nullptr;
 }
 
 size_t slha_model_dim(const SlhaModel* model) {
@@ -597,16 +739,24 @@ int32_t slha_encode_key(const SlhaModel* model, const float* key, size_t d, uint
         std::vector<float> kv(d);
         std::memcpy(kv.data(), key, d * sizeof(float));
         validate_finite(kv.data(), d, "key");
-        auto zb = m->device_buffers();
         hipStream_t s;
-        char* base = staging(1024, &s);
-        check_hip(hipMemcpyAsync(base, kv.data(), 512, hipMemcpyHostToDevice, s), "H2D key");
-        check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, position, codec, m->residual_mode, 0,
-                                zb.z, zb.zpack, zb.cert_scale, zb.diag, lambda_c(), rht_inv(),
-                                base + 512, s),
-                  "encode kernel");
+        const size_t kb = align256(d * sizeof(float));
+        char* base = staging(kb + 256, &s);
+        check_hip(hipMemcpyAsync(base, kv.data(), d * sizeof(float), hipMemcpyHostToDevice, s),
+                  "H2D key");
+        if (m->learned) {  // LearnedModel::encode_with (learned.rs:353-408)
+            check_hip(launch_learned_encode(base, kDtypeF32, 1, 1, 1, position, codec, 0,
+                                            m->learned_projection(), lambda_c(), base + kb, s),
+                      "learned encode kernel");
+        } else {
+            auto zb = m->device_buffers();
+            check_hip(launch_encode(base, kDtypeF32, 1, 1, 1, position, codec, m->residual_mode, 0,
+                                    zb.z, zb.zpack, zb.cert_scale, zb.diag, lambda_c(), rht_inv(),
+                                    base + kb, s),
+                      "encode kernel");
+        }
         SciRustSlhaTile t;
-        check_hip(hipMemcpyAsync(&t, base + 512, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
+        check_hip(hipMemcpyAsync(&t, base + kb, sizeof t, hipMemcpyDeviceToHost, s), "D2H tile");
         check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
         validate_tile(t);
         std::memcpy(out_tile, &t, sizeof t);
@@ -622,18 +772,24 @@ static int32_t decode_common(const SlhaModel* model, const SciRustSlhaTile* tile
             fail(SLHA_ERR_DIMENSION, "output dimension mismatch: received %zu, expected %zu", d, m->d);
         const SciRustSlhaTile t = read_tile(tile);
         validate_tile(t);
-        auto zb = m->device_buffers();
         hipStream_t s;
-        char* base = staging(1024, &s);
+        char* base = staging(256 + align256(d * sizeof(float)), &s);
+        float* od = reinterpret_cast<float*>(base + 256);
         check_hip(hipMemcpyAsync(base, &t, sizeof t, hipMemcpyHostToDevice, s), "H2D tile");
-        const float* z = (with_residual && !m->rht) ? zb.z : nullptr;
-        check_hip(launch_decode(base, 1, z, sqrt_half_pi(), reinterpret_cast<float*>(base + 512), s),
-                  "decode kernel");
-        float v[128];
-        check_hip(hipMemcpyAsync(v, base + 512, sizeof v, hipMemcpyDeviceToHost, s), "D2H");
+        if (m->learned) {  // reconstruct / reconstruct_from_tile (learned.rs:276-320)
+            check_hip(launch_learned_decode(base, 1, m->learned_projection(), with_residual ? 1 : 0,
+                                            sqrt_half_pi(), od, s),
+                      "learned decode kernel");
+        } else {
+            auto zb = m->device_buffers();
+            const float* z = (with_residual && !m->rht) ? zb.z : nullptr;
+            check_hip(launch_decode(base, 1, z, sqrt_half_pi(), od, s), "decode kernel");
+        }
+        std::vector<float> v(d);
+        check_hip(hipMemcpyAsync(v.data(), od, d * sizeof(float), hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-        validate_finite(v, 128, with_residual ? "reconstruction" : "dequantized_latent");
-        std::memcpy(out, v, sizeof v);
+        validate_finite(v.data(), d, with_residual || m->learned ? "reconstruction" : "dequantized_latent");
+        std::memcpy(out, v.data(), d * sizeof(float));
     });
 }
 
@@ -704,6 +860,25 @@ int32_t slha_model_projection(const SlhaModel* model, float* z_out, float* rht_d
     });
 }
 
+size_t slha_model_pad_dim(const SlhaModel* model) {
+    size_t d_pad = 0;
+    const int32_t rc = ffi_status([&] { d_pad = model_of(model)->d_pad; });
+    return rc == SLHA_OK ? d_pad : 0;
+}
+
+int32_t slha_model_latent_projection(const SlhaModel* model, float* p_out) {
+    return ffi_status([&] {
+        if (!p_out) fail(SLHA_ERR_NULL, "p_out is NULL");
+        auto m = model_of(model);
+        if (!m->learned) {  // identity latent
+            std::memset(p_out, 0, 128 * 128 * sizeof(float));
+            for (int k = 0; k < 128; ++k) p_out[k * 128 + k] = 1.0f;
+            return;
+        }
+        std::memcpy(p_out, m->p.data(), m->p.size() * sizeof(float));
+    });
+}
+
 int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t key_dtype,
                         size_t n_rows, size_t n_tok, size_t n_kv_heads, uint32_t pos0,
                         int32_t codec, int32_t warm, SciRustSlhaTile* tiles_dev, void* stream) {
@@ -721,6 +896,14 @@ int32_t slha_gpu_encode(const SlhaModel* model, const void* keys_dev, int32_t ke
         if (n == 0) return;
         if (!keys_dev || !tiles_dev) fail(SLHA_ERR_NULL, "slha_gpu_encode received a NULL pointer");
         require_device();
+        if (m->learned) {
+            check_hip(launch_learned_encode(keys_dev, key_dtype, n, (uint32_t)n_tok,
+                                            (uint32_t)n_kv_heads, pos0, codec, warm,
+                                            m->learned_projection(), lambda_c(), tiles_dev,
+                                            static_cast<hipStream_t>(stream)),
+                      "learned encode kernel");
+            return;
+        }
         auto zb = m->device_buffers();
         check_hip(launch_encode(keys_dev, key_dtype, n, (uint32_t)n_tok, (uint32_t)n_kv_heads, pos0,
                                 codec, m->residual_mode, warm, zb.z, zb.zpack, zb.cert_scale,
@@ -741,6 +924,13 @@ int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int3
         if (!q_dev || !q_coarse_dev || !q_sign_dev)
             fail(SLHA_ERR_NULL, "slha_gpu_prepare_queries received a NULL pointer");
         require_device();
+        if (m->learned) {
+            check_hip(launch_learned_prepare(q_dev, q_dtype, n_q, m->learned_projection(),
+                                             q_coarse_dev, q_sign_dev,
+                                             static_cast<hipStream_t>(stream)),
+                      "learned prepare kernel");
+            return;
+        }
         auto zb = m->device_buffers();
         check_hip(launch_prepare_queries(q_dev, q_dtype, n_q, zb.z, zb.diag, rht_inv(),
                                          q_coarse_dev, q_sign_dev, static_cast<hipStream_t>(stream)),
@@ -793,6 +983,13 @@ int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev
         if (n == 0) return;
         if (!tiles_dev || !out_dev) fail(SLHA_ERR_NULL, "slha_gpu_decode received a NULL pointer");
         require_device();
+        if (m->learned) {
+            check_hip(launch_learned_decode(tiles_dev, n, m->learned_projection(),
+                                            with_residual ? 1 : 0, sqrt_half_pi(), out_dev,
+                                            static_cast<hipStream_t>(stream)),
+                      "learned decode kernel");
+            return;
+        }
         auto zb = m->device_buffers();
         const float* z = (with_residual && !m->rht) ? zb.z : nullptr;
         check_hip(launch_decode(tiles_dev, n, z, sqrt_half_pi(), out_dev,

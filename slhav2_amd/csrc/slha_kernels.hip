@@ -2274,6 +2274,219 @@ __global__ __launch_bounds__(256) void ccos_apply_kernel(uint4* __restrict__ til
 }
 
 // ---------------------------------------------------------------------------
+// Learned models (d > 128): LearnedModel built from a .slhw projection
+// (learned.rs:218-257, weights.rs:159-270). P is [128][d] row-major with
+// per-component scale 1 (so h_k / s_k and h_k * s_k are exact no-ops), Z is
+// [256][d_pad] and the optional RHT diagonal is [d_pad], d_pad = next_pow2(d)
+// with RHT and d without (incoherence.rs:29-35, 89-98).
+//
+// One workgroup of 256 threads per vector. Every sum keeps the reference's
+// sequential f32 order (mul then add, no contraction), so latent codes, sign
+// bits and reconstructions are bit-exact:
+//   latent   h_k = sum_i P[k][i] key[i]          thread k < 128   (evec_dot, learned.rs:257-273)
+//   recon    r_i = sum_k h_k P[k][i]             one thread per i (reconstruct, learned.rs:276-286)
+//   sigma    sqrt((sum_i e_i e_i) / d), f32      thread 0         (encode_with, learned.rs:398)
+//   sketch   bit s = (sum_i Z[s][i] buf[i] < 0)  thread s         (sign_bits, learned.rs:326-347)
+// where e = key - r and buf = e, or FWHT(diag . pad(e)) / sqrt(d_pad)
+// (transform_into, incoherence.rs:114-125; fwht_inplace, :45-70). The FWHT
+// runs stage by stage in LDS; each butterfly is the same IEEE add/sub as in
+// the sequential loop, so the order of pairs within a stage does not matter.
+
+struct LearnedArgs {
+    const float* p;     // [128][d]
+    const float* z;     // [256][d_pad]
+    const float* diag;  // [d_pad] +-1, or null without RHT
+    uint32_t d, d_pad;
+    float rht_inv;      // 1 / sqrt(d_pad)
+};
+
+// Dynamic LDS of the learned kernels: vec[d], buf[d_pad], h[128], 32 words.
+__host__ __device__ constexpr size_t learned_lds_bytes(uint32_t d, uint32_t d_pad) {
+    return ((size_t)d + d_pad + 128 + 32) * 4;
+}
+
+// Sequential f32 dot product sum_i row[i] * v[i], i = 0 .. n-1 (v in LDS).
+__device__ __forceinline__ float seq_dot(const float* __restrict__ row, const float* v, uint32_t n) {
+    float acc = 0.0f;
+    uint32_t i = 0;
+    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+        for (; i + 4 <= n; i += 4) {
+            const float4 r = *reinterpret_cast<const float4*>(row + i);
+            acc += r.x * v[i];
+            acc += r.y * v[i + 1];
+            acc += r.z * v[i + 2];
+            acc += r.w * v[i + 3];
+        }
+    }
+    for (; i < n; ++i) acc += row[i] * v[i];
+    return acc;
+}
+
+__device__ __forceinline__ void lds_load_vec(const void* __restrict__ src, int dtype, uint64_t idx,
+                                             uint32_t d, float* out) {
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x)
+        out[i] = dtype == kDtypeBF16
+                     ? __uint_as_float((uint32_t)static_cast<const uint16_t*>(src)[idx * d + i] << 16)
+                     : static_cast<const float*>(src)[idx * d + i];
+}
+
+// buf <- FWHT(diag . buf) / sqrt(d_pad), in place in LDS (all threads).
+__device__ __forceinline__ void block_rht(float* buf, const float* __restrict__ diag,
+                                          uint32_t d_pad, float inv) {
+    for (uint32_t i = threadIdx.x; i < d_pad; i += blockDim.x) buf[i] *= diag[i];
+    __syncthreads();
+    for (uint32_t h = 1; h < d_pad; h <<= 1) {
+        for (uint32_t q = threadIdx.x; q < d_pad / 2; q += blockDim.x) {
+            const uint32_t j = ((q & ~(h - 1u)) << 1) | (q & (h - 1u));  // pair (j, j + h)
+            const float a = buf[j], b = buf[j + h];
+            buf[j] = a + b;
+            buf[j + h] = a - b;
+        }
+        __syncthreads();
+    }
+    for (uint32_t i = threadIdx.x; i < d_pad; i += blockDim.x) buf[i] *= inv;
+    __syncthreads();
+}
+
+// words[0..7] <- sign bits of Z . buf (bit s = 1 iff the sum is negative);
+// thread s computes row s, wave w's ballot is u64 word w. blockDim.x == 256.
+__device__ __forceinline__ void block_sign_bits(const float* buf, const float* __restrict__ z,
+                                                uint32_t d_pad, uint32_t* words) {
+    const uint32_t s = threadIdx.x;
+    const float acc = seq_dot(z + (size_t)s * d_pad, buf, d_pad);
+    const uint64_t m = __ballot(acc < 0.0f);
+    if ((s & 63u) == 0) {
+        words[2 * (s >> 6)] = (uint32_t)m;
+        words[2 * (s >> 6) + 1] = (uint32_t)(m >> 32);
+    }
+}
+
+// Key -> tile (encode_with, learned.rs:353-408). Keys [n][d]; key i is token
+// t = i % n_tok of row i / n_tok: token_id = position = pos0 + t, head_id =
+// row % n_kv (head 0 for a single key, as the reference).
+template <int CODEC>
+__global__ __launch_bounds__(256) void learned_encode_kernel(const void* __restrict__ keys, int dtype,
+                                                             uint64_t n_keys, uint32_t n_tok,
+                                                             uint32_t n_kv, uint32_t pos0, int warm,
+                                                             LearnedArgs a, float lambda_c,
+                                                             uint4* __restrict__ tiles) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* key = lds;
+    float* buf = lds + a.d;
+    float* h = buf + a.d_pad;
+    uint32_t* misc = reinterpret_cast<uint32_t*>(h + 128);  // sign words 0..7, sigma 8
+    const uint32_t tid = threadIdx.x;
+    for (uint64_t ki = blockIdx.x; ki < n_keys; ki += gridDim.x) {
+        lds_load_vec(keys, dtype, ki, a.d, key);
+        __syncthreads();
+        if (tid < 128) h[tid] = seq_dot(a.p + (size_t)tid * a.d, key, a.d);
+        __syncthreads();
+        // Residual from the un-quantised latent.
+        for (uint32_t i = tid; i < a.d; i += blockDim.x) {
+            float r = 0.0f;
+            for (uint32_t k = 0; k < 128; ++k) r += h[k] * a.p[(size_t)k * a.d + i];
+            buf[i] = key[i] - r;
+        }
+        for (uint32_t i = a.d + tid; i < a.d_pad; i += blockDim.x) buf[i] = 0.0f;
+        __syncthreads();
+        if (tid == 0) {
+            float acc = 0.0f;
+            for (uint32_t i = 0; i < a.d; ++i) acc += buf[i] * buf[i];
+            misc[8] = __float_as_uint(sqrtf(acc / (float)a.d));
+        }
+        __syncthreads();  // sigma has read buf before the RHT rewrites it
+        if (a.diag) block_rht(buf, a.diag, a.d_pad, a.rht_inv);
+        block_sign_bits(buf, a.z, a.d_pad, misc);
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t lw[16], gsw[2];
+            float scale;
+            const uint32_t codec_flag = quantize<CODEC>(h, lw, &scale, gsw);
+            const float sigma = __uint_as_float(misc[8]);
+            const float lambda = sigma * lambda_c;
+            const uint32_t row = (uint32_t)(ki / n_tok);
+            const uint32_t pos = pos0 + (uint32_t)(ki - (uint64_t)row * n_tok);
+            const uint32_t flags = codec_flag | (warm ? kFlagWarm : 0u);
+            uint4* out = tiles + ki * 8;
+            out[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            out[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+            out[2] = make_uint4(lw[8], lw[9], lw[10], lw[11]);
+            out[3] = make_uint4(lw[12], lw[13], lw[14], lw[15]);
+            out[4] = make_uint4(misc[0], misc[1], misc[2], misc[3]);
+            out[5] = make_uint4(misc[4], misc[5], misc[6], misc[7]);
+            out[6] = make_uint4(__float_as_uint(scale), __float_as_uint(lambda), misc[8], pos);
+            out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
+        }
+        __syncthreads();
+    }
+}
+
+// Query -> (q_coarse [128], q_sign [4]) (slha_prepare_query, lib.rs:420-463:
+// query_coarse, learned.rs:267-273, and sign_bits of the query itself).
+__global__ __launch_bounds__(256) void learned_prepare_kernel(const void* __restrict__ q, int dtype,
+                                                              uint64_t n_q, LearnedArgs a,
+                                                              float* __restrict__ qc,
+                                                              uint64_t* __restrict__ qs) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* vec = lds;
+    float* buf = lds + a.d;
+    uint32_t* words = reinterpret_cast<uint32_t*>(buf + a.d_pad + 128);
+    const uint32_t tid = threadIdx.x;
+    for (uint64_t qi = blockIdx.x; qi < n_q; qi += gridDim.x) {
+        lds_load_vec(q, dtype, qi, a.d, vec);
+        __syncthreads();
+        for (uint32_t i = tid; i < a.d_pad; i += blockDim.x) buf[i] = i < a.d ? vec[i] : 0.0f;
+        if (tid < 128) qc[qi * 128 + tid] = seq_dot(a.p + (size_t)tid * a.d, vec, a.d);
+        __syncthreads();
+        if (a.diag) block_rht(buf, a.diag, a.d_pad, a.rht_inv);
+        block_sign_bits(buf, a.z, a.d_pad, words);
+        __syncthreads();
+        if (tid < 4) qs[qi * 4 + tid] = (uint64_t)words[2 * tid] | ((uint64_t)words[2 * tid + 1] << 32);
+        __syncthreads();
+    }
+}
+
+// Tile -> key estimate [d]: reconstruct(dequant_latent) (slha_decode_latent,
+// lib.rs:763-822), plus with_residual the sign-sketch term of
+// reconstruct_from_tile (learned.rs:288-320), omitted for RHT models.
+__global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __restrict__ tiles,
+                                                             uint64_t n, LearnedArgs a,
+                                                             int with_residual, float sqrt_half_pi,
+                                                             float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* h = lds;
+    uint32_t* misc = reinterpret_cast<uint32_t*>(h + 128);  // residual words 0..7, sigma 8
+    const uint32_t tid = threadIdx.x;
+    const bool resid = with_residual && !a.diag;
+    for (uint64_t ti = blockIdx.x; ti < n; ti += gridDim.x) {
+        if (tid == 0) {
+            uint32_t w[32];
+            load_tile(tiles + ti * 8, w);
+            float k[kDC];
+            dequant_exact(w, w + 30, __uint_as_float(w[24]), w[29] >> 16, k);
+            for (int d = 0; d < kDC; ++d) h[d] = k[d];
+            for (int j = 0; j < 8; ++j) misc[j] = w[16 + j];
+            misc[8] = w[26];
+        }
+        __syncthreads();
+        // (sigma * sqrt(pi/2)) / 256, learned.rs:303
+        const float sc = __uint_as_float(misc[8]) * sqrt_half_pi / 256.0f;
+        for (uint32_t i = tid; i < a.d; i += blockDim.x) {
+            float r = 0.0f;
+            for (uint32_t k = 0; k < 128; ++k) r += h[k] * a.p[(size_t)k * a.d + i];
+            if (resid) {
+                for (uint32_t s = 0; s < kDS; ++s) {
+                    const float sgn = ((misc[s >> 5] >> (s & 31u)) & 1u) ? -1.0f : 1.0f;
+                    r += sgn * sc * a.z[(size_t)s * a.d_pad + i];
+                }
+            }
+            out[ti * a.d + i] = r;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Launchers
 
 size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
@@ -2457,6 +2670,68 @@ hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, 
     if (n == 0) return hipSuccess;
     decode_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<const uint4*>(tiles), n,
                                                              z_or_null, sqrt_half_pi, out);
+    return hipGetLastError();
+}
+
+namespace {
+LearnedArgs learned_args(const LearnedProjection& lp) {
+    return LearnedArgs{lp.p, lp.z, lp.diag, lp.d, lp.d_pad, lp.rht_inv};
+}
+unsigned learned_grid(uint64_t n) { return (unsigned)std::min<uint64_t>(n, 1u << 20); }
+// Dynamic LDS above the default 64 KiB needs the kernel's opt-in.
+template <typename K>
+hipError_t allow_lds(K kernel, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+}  // namespace
+
+hipError_t launch_learned_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
+                                 uint32_t n_kv, uint32_t pos0, int codec, int warm,
+                                 const LearnedProjection& lp, float lambda_c, void* tiles,
+                                 hipStream_t s) {
+    if (n_keys == 0) return hipSuccess;
+    const size_t lds = learned_lds_bytes(lp.d, lp.d_pad);
+    uint4* out = static_cast<uint4*>(tiles);
+    const LearnedArgs a = learned_args(lp);
+#define SLHA_LEARNED_ENC(C)                                                                        \
+    {                                                                                              \
+        const hipError_t e = allow_lds(learned_encode_kernel<C>, lds);                              \
+        if (e != hipSuccess) return e;                                                             \
+        learned_encode_kernel<C><<<learned_grid(n_keys), 256, lds, s>>>(keys, dtype, n_keys, n_tok, \
+                                                                        n_kv, pos0, warm, a,       \
+                                                                        lambda_c, out);            \
+        break;                                                                                     \
+    }
+    switch (codec) {
+        case kCodecInt4Single: SLHA_LEARNED_ENC(kCodecInt4Single)
+        case kCodecInt4Grouped: SLHA_LEARNED_ENC(kCodecInt4Grouped)
+        case kCodecNF4: SLHA_LEARNED_ENC(kCodecNF4)
+        case kCodecMixed: SLHA_LEARNED_ENC(kCodecMixed)
+        case kCodecTQ3: SLHA_LEARNED_ENC(kCodecTQ3)
+        case kCodecMix3: SLHA_LEARNED_ENC(kCodecMix3)
+        default: return hipErrorInvalidValue;
+    }
+#undef SLHA_LEARNED_ENC
+    return hipGetLastError();
+}
+
+hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const LearnedProjection& lp,
+                                  float* qc, uint64_t* qs, hipStream_t s) {
+    if (n_q == 0) return hipSuccess;
+    const size_t lds = learned_lds_bytes(lp.d, lp.d_pad);
+    const hipError_t e = allow_lds(learned_prepare_kernel, lds);
+    if (e != hipSuccess) return e;
+    learned_prepare_kernel<<<learned_grid(n_q), 256, lds, s>>>(q, dtype, n_q, learned_args(lp), qc, qs);
+    return hipGetLastError();
+}
+
+hipError_t launch_learned_decode(const void* tiles, uint64_t n, const LearnedProjection& lp,
+                                 int with_residual, float sqrt_half_pi, float* out, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    learned_decode_kernel<<<learned_grid(n), 256, (128 + 32) * 4, s>>>(
+        static_cast<const uint4*>(tiles), n, learned_args(lp), with_residual, sqrt_half_pi, out);
     return hipGetLastError();
 }
 

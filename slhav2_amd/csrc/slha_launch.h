@@ -54,6 +54,31 @@ float build_projection_pack(const float* z, void* pack);
 hipError_t launch_prepare_queries(const void* q, int dtype, uint64_t n_q, const float* z,
                                   const float* diag, float rht_inv, float* qc, uint64_t* qs,
                                   hipStream_t s);
+// Learned (d > 128) models: P [128][d], Z [256][d_pad], RHT diagonal [d_pad]
+// or null, d_pad = next_pow2(d) with RHT, else d. The kernels keep a vector
+// and its padded residual in LDS: d_pad <= kLearnedMaxDPad.
+struct LearnedProjection {
+    const float* p = nullptr;
+    const float* z = nullptr;
+    const float* diag = nullptr;
+    uint32_t d = 0, d_pad = 0;
+    float rht_inv = 1.0f;
+};
+constexpr uint32_t kLearnedMaxDPad = 16384;
+// keys [n_keys][d] (f32 or bf16) -> tiles, bit-exact with encode_with
+// (learned.rs:353-408); key i: token_id = position = pos0 + i % n_tok,
+// head_id = (i / n_tok) % n_kv.
+hipError_t launch_learned_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
+                                 uint32_t n_kv, uint32_t pos0, int codec, int warm,
+                                 const LearnedProjection& lp, float lambda_c, void* tiles,
+                                 hipStream_t s);
+// q [n_q][d] -> q_coarse [n_q][128], q_sign [n_q][4].
+hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const LearnedProjection& lp,
+                                  float* qc, uint64_t* qs, hipStream_t s);
+// tiles [n] -> out [n][d] (reconstruct; with_residual adds the sign-sketch
+// estimate when the model has no RHT).
+hipError_t launch_learned_decode(const void* tiles, uint64_t n, const LearnedProjection& lp,
+                                 int with_residual, float sqrt_half_pi, float* out, hipStream_t s);
 hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, float sqrt_half_pi,
                          float* out, hipStream_t s);
 hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s);

@@ -79,6 +79,13 @@ for name, res, args in [
     ("orc_page_out", None, [_P]),
     ("orc_drop_correction", ctypes.c_int, [_P]),
     ("orc_topk", None, [_P, _SZ, _SZ, _P, _P]),
+    ("orc_learned_latent", None, [_P, _SZ, _P, _P]),
+    ("orc_learned_query_coarse", None, [_P, _SZ, _P, _P]),
+    ("orc_learned_reconstruct", None, [_P, _SZ, _P, _P]),
+    ("orc_learned_query", None, [_P, _P, _P, _SZ, _SZ, _P, _P, _P]),
+    ("orc_learned_encode", ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, ctypes.c_uint32, ctypes.c_int,
+                                          ctypes.c_int, _P]),
+    ("orc_learned_decode", None, [_P, _P, _SZ, _SZ, ctypes.c_int, _P, ctypes.c_int, _P]),
 ]:
     fn = getattr(lib, name)
     fn.restype = res
@@ -250,3 +257,58 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     return r.astype(np.uint32).view(np.float32)
+
+
+class Learned:
+    """The oracle's LearnedModel (learned.rs:257-408) over a loaded projection:
+    p [128][d], z [256][d_pad], diag [d_pad] or None."""
+
+    def __init__(self, p, z, diag=None):
+        self.p = f32(p)
+        self.z = f32(z)
+        self.diag = f32(diag) if diag is not None else None
+        self.d = self.p.shape[1]
+        self.d_pad = self.z.shape[1]
+        assert self.p.shape[0] == 128 and self.z.shape[0] == 256
+
+    def _diag(self):
+        return _p(self.diag) if self.diag is not None else None
+
+    def latent(self, key) -> np.ndarray:
+        k = f32(key)
+        h = np.zeros(128, np.float32)
+        lib.orc_learned_latent(_p(self.p), self.d, _p(k), _p(h))
+        return h
+
+    def reconstruct(self, h) -> np.ndarray:
+        h = f32(h)
+        out = np.zeros(self.d, np.float32)
+        lib.orc_learned_reconstruct(_p(self.p), self.d, _p(h), _p(out))
+        return out
+
+    def query(self, q) -> tuple[np.ndarray, np.ndarray]:
+        q = f32(q)
+        qc = np.zeros(128, np.float32)
+        qs = np.zeros(4, np.uint64)
+        lib.orc_learned_query(_p(self.p), _p(self.z), self._diag(), self.d, self.d_pad, _p(q),
+                              _p(qc), _p(qs))
+        return qc, qs
+
+    def encode(self, keys, codec: int, pos0: int = 0, warm: int = 0) -> np.ndarray:
+        k = f32(keys).reshape(-1, self.d)
+        out = np.zeros(len(k), TILE_DTYPE)
+        for i in range(len(k)):
+            row = np.ascontiguousarray(k[i])
+            rc = lib.orc_learned_encode(_p(self.p), _p(self.z), self._diag(), self.d, self.d_pad,
+                                        _p(row), pos0 + i, codec, warm, out[i:i + 1].ctypes.data)
+            assert rc == 0, rc
+        return out
+
+    def decode(self, tiles, with_residual: bool) -> np.ndarray:
+        t = np.ascontiguousarray(tiles, TILE_DTYPE).reshape(-1)
+        out = np.zeros((len(t), self.d), np.float32)
+        for i in range(len(t)):
+            lib.orc_learned_decode(_p(self.p), _p(self.z), self.d, self.d_pad,
+                                   int(self.diag is not None), t[i:i + 1].ctypes.data,
+                                   int(with_residual), out[i].ctypes.data)
+        return out

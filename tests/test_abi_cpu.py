@@ -99,7 +99,7 @@ def test_weights_load_errors():
     assert not s.lib.slha_weights_load(None) and "NULL" in s.last_error()
     assert not s.lib.slha_weights_load(b"\xff\xfe.slhw") and "UTF-8" in s.last_error()
     assert not s.lib.slha_weights_load(b"/nonexistent/model.slhw")
-    assert "not supported" in s.last_error()
+    assert "weights: cannot stat /nonexistent/model.slhw" in s.last_error()
 
 
 def test_dimension_and_codec_errors_precede_any_device_work():
