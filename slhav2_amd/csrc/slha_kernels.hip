@@ -1890,6 +1890,7 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
 // 16kb+c.
 
 constexpr uint32_t kEncQueue = 256;  // queued (key, bit) recomputations per wave
+constexpr uint32_t kEncZAhead = 2;   // Z row blocks in flight ahead of the MFMAs (divides 16)
 constexpr uint32_t kEncQueueKey = 32;  // keys with more uncertain bits keep them
 
 struct EncWaveLds {
@@ -2024,70 +2025,71 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
     }
     const uint4* zp = zpack + lane;
     uint32_t wp[4] = {0u, 0u, 0u, 0u}, up[4] = {0u, 0u, 0u, 0u};
-    // Z operands of block sb; the next block's are in flight while this one
-    // is multiplied.
-    uint4 ah[4], am[4], nh[4], nm[4];
+    // Z operands of kEncZAhead row blocks in flight: block sb's 8 loads go
+    // out kEncZAhead blocks before it is multiplied, so their L2 latency is
+    // covered by that many blocks of MFMAs (the kernel runs one wave per SIMD,
+    // so no other wave hides it). The ring is indexed statically inside the
+    // unrolled inner loop.
+    uint4 zr[kEncZAhead][8];
 #pragma unroll
-    for (uint32_t ks = 0; ks < 4; ++ks) {
-        ah[ks] = zp[(ks * 2u + 0u) * 64u];
-        am[ks] = zp[(ks * 2u + 1u) * 64u];
-    }
-#pragma unroll 2
-    for (uint32_t sb = 0; sb < 16; ++sb) {
-        const uint32_t sn = sb + 1u < 16u ? sb + 1u : sb;
+    for (uint32_t j = 0; j < kEncZAhead; ++j)
 #pragma unroll
-        for (uint32_t ks = 0; ks < 4; ++ks) {
-            nh[ks] = zp[((sn * 4u + ks) * 2u + 0u) * 64u];
-            nm[ks] = zp[((sn * 4u + ks) * 2u + 1u) * 64u];
-        }
-        v4f acc[4];
+        for (uint32_t o = 0; o < 8; ++o) zr[j][o] = zp[(j * 8u + o) * 64u];
+    for (uint32_t sb0 = 0; sb0 < 16; sb0 += kEncZAhead) {
 #pragma unroll
-        for (uint32_t kb = 0; kb < 4; ++kb) acc[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        // Four independent accumulation chains, interleaved.
+        for (uint32_t j = 0; j < kEncZAhead; ++j) {
+            const uint32_t sb = sb0 + j;
+            v4f acc[4];
 #pragma unroll
-        for (uint32_t ks = 0; ks < 4; ++ks) {
-            const v8bf a_h = __builtin_bit_cast(v8bf, ah[ks]);
-            const v8bf a_m = __builtin_bit_cast(v8bf, am[ks]);
+            for (uint32_t kb = 0; kb < 4; ++kb) acc[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            // Four independent accumulation chains, interleaved.
+#pragma unroll
+            for (uint32_t ks = 0; ks < 4; ++ks) {
+                const v8bf a_h = __builtin_bit_cast(v8bf, zr[j][2 * ks]);
+                const v8bf a_m = __builtin_bit_cast(v8bf, zr[j][2 * ks + 1]);
+#pragma unroll
+                for (uint32_t kb = 0; kb < 4; ++kb) {
+                    const v8bf b_h = __builtin_bit_cast(
+                        v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
+                    acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_h, acc[kb], 0, 0, 0);
+                }
+#pragma unroll
+                for (uint32_t kb = 0; kb < 4; ++kb) {
+                    const v8bf b_m = __builtin_bit_cast(
+                        v8bf, make_uint4(bm[kb][ks][0], bm[kb][ks][1], bm[kb][ks][2], bm[kb][ks][3]));
+                    acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_m, acc[kb], 0, 0, 0);
+                }
+#pragma unroll
+                for (uint32_t kb = 0; kb < 4; ++kb) {
+                    const v8bf b_h = __builtin_bit_cast(
+                        v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
+                    acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_m, b_h, acc[kb], 0, 0, 0);
+                }
+            }
+            // Refill this slot with block sb + kEncZAhead; the barrier keeps
+            // the loads here instead of next to their use.
+            if (sb + kEncZAhead < 16u) {
+#pragma unroll
+                for (uint32_t o = 0; o < 8; ++o) zr[j][o] = zp[((sb + kEncZAhead) * 8u + o) * 64u];
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (uint32_t kb = 0; kb < 4; ++kb) {
-                const v8bf b_h = __builtin_bit_cast(
-                    v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
-                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_h, acc[kb], 0, 0, 0);
-            }
+                uint32_t nib = 0u, u = 0u;
 #pragma unroll
-            for (uint32_t kb = 0; kb < 4; ++kb) {
-                const v8bf b_m = __builtin_bit_cast(
-                    v8bf, make_uint4(bm[kb][ks][0], bm[kb][ks][1], bm[kb][ks][2], bm[kb][ks][3]));
-                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, b_m, acc[kb], 0, 0, 0);
+                for (uint32_t r = 0; r < 4; ++r) {
+                    nib |= (acc[kb][r] < 0.0f ? 1u : 0u) << r;
+                    u |= (fabsf(acc[kb][r]) > bk[kb] ? 0u : 1u) << r;
+                }
+                const uint32_t sh = 4u * g + ((sb & 1u) ? 16u : 0u);
+                wp[kb] = ((sb & 1u) ? wp[kb] : 0u) | (nib << sh);
+                up[kb] = ((sb & 1u) ? up[kb] : 0u) | (u << sh);
+                if (sb & 1u) {
+                    const uint32_t w = (16u * kb + c) * 8u + (sb >> 1);
+                    atomicOr(&W.bits[w], wp[kb]);
+                    if (up[kb] != 0u) atomicOr(&W.umask[w], up[kb]);
+                }
             }
-#pragma unroll
-            for (uint32_t kb = 0; kb < 4; ++kb) {
-                const v8bf b_h = __builtin_bit_cast(
-                    v8bf, make_uint4(bh[kb][ks][0], bh[kb][ks][1], bh[kb][ks][2], bh[kb][ks][3]));
-                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_m, b_h, acc[kb], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (uint32_t kb = 0; kb < 4; ++kb) {
-            uint32_t nib = 0u, u = 0u;
-#pragma unroll
-            for (uint32_t r = 0; r < 4; ++r) {
-                nib |= (acc[kb][r] < 0.0f ? 1u : 0u) << r;
-                u |= (fabsf(acc[kb][r]) > bk[kb] ? 0u : 1u) << r;
-            }
-            const uint32_t sh = 4u * g + ((sb & 1u) ? 16u : 0u);
-            wp[kb] = ((sb & 1u) ? wp[kb] : 0u) | (nib << sh);
-            up[kb] = ((sb & 1u) ? up[kb] : 0u) | (u << sh);
-            if (sb & 1u) {
-                const uint32_t w = (16u * kb + c) * 8u + (sb >> 1);
-                atomicOr(&W.bits[w], wp[kb]);
-                if (up[kb] != 0u) atomicOr(&W.umask[w], up[kb]);
-            }
-        }
-#pragma unroll
-        for (uint32_t ks = 0; ks < 4; ++ks) {
-            ah[ks] = nh[ks];
-            am[ks] = nm[ks];
         }
     }
     __syncthreads();
