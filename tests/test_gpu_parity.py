@@ -159,6 +159,42 @@ def test_encode_sign_fallback_paths(s, torch, rht):
                 raise AssertionError((codec, rht, diff[:10]))
 
 
+def boundary_keys(n, seed):
+    """Keys whose elements sit on, or one or two ulps from, the codecs'
+    rounding boundaries: with max |k| = 7 (INT4 step 1) every half-integer
+    is a roundf tie; with group maxima of 3.5 (TQ3 step 1) the elements are
+    on or next to t + 3.5 = k + 1/2 and to the correction levels k - 3.5."""
+    r = np.random.default_rng(seed)
+    half = np.arange(-7, 7, dtype=np.float32) + np.float32(0.5)   # INT4 ties
+    tq3 = np.concatenate([np.arange(-4, 4, dtype=np.float32),        # t + 3.5 half-integers
+                          np.arange(0, 8, dtype=np.float32) - np.float32(3.5)])  # levels
+    base = np.concatenate([half, tq3]).astype(np.float32)
+    keys = r.choice(base, size=(n, 128)).astype(np.float32)
+    nudge = r.integers(-2, 3, size=(n, 128))
+    keys = np.nextafter(keys, np.where(nudge > 0, np.inf, -np.inf).astype(np.float32))
+    keys = np.where(nudge == 0, r.choice(base, size=(n, 128)), keys).astype(np.float32)
+    keys[:, 0] = 7.0                 # fix the INT4 step at 1
+    keys[:, 16::16] = 3.5            # and each TQ3 group's step at 1
+    keys[n // 2:] *= np.float32(0.37)  # non-unit steps too
+    return keys
+
+
+@pytest.mark.parametrize("rht", [False, True])
+def test_encode_rounding_boundaries_bit_exact(s, torch, rht):
+    """Codes (roundf ties to the larger magnitude, TQ3 correction bits at
+    their levels) equal the oracle's for keys built on and around every
+    rounding boundary."""
+    keys = boundary_keys(512, 9)
+    with s.Model(seed=78, rht=rht) as m:
+        z, diag = m.projection()
+        d = diag if rht else None
+        for codec in (0, 1, 4):
+            print(f"boundary keys codec={codec} rht={rht}", flush=True)
+            got = tiles_np(s.gpu_encode(m, dev(torch, keys), codec))
+            ref = o.encode(keys, codec, 1, z, d)
+            assert got.tobytes() == ref.tobytes(), codec
+
+
 def test_encode_c4_size_bit_exact(s, torch):
     # C4-like keys (N(0,1) x log-uniform scale, bf16), TQ3 + RHT, 131072 keys:
     # every tile byte against the oracle.
