@@ -327,6 +327,52 @@ def run_c4(args) -> int:
     return 0
 
 
+def run_decode(args) -> int:
+    """Decode attention over compressed keys at the C2 shape (benchmark_decode.rs:
+    29-90 on the GPU): 8 KV heads x 32 768 INT4 tiles, bf16 V [8, 32768, 128],
+    32 query heads in GQA groups of 4; one step = slha_gpu_decode_attention
+    (scores, softmax(s / sqrt(128)), sum w V). Four KV sets (tiles + V,
+    384 MiB) are rotated so a step reads HBM."""
+    import numpy as np
+    import torch
+
+    import slhav2_amd as s
+
+    n_sets, d_v = 4, 128
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0007)
+    model = s.Model(seed=0x5EED0002, rht=False, residual_mode=s.RESIDUAL_R)
+    queries = torch.randn((N_Q, D), device="cuda", generator=g).to(torch.bfloat16)
+    qc, qs = s.gpu_prepare_queries(model, queries)
+    sets = []
+    for _ in range(n_sets):
+        keys = torch.randn((N_KV, N_TOK, D), device="cuda", generator=g).to(torch.bfloat16)
+        vals = torch.randn((N_KV, N_TOK, d_v), device="cuda", generator=g).to(torch.bfloat16)
+        sets.append((s.gpu_encode(model, keys, s.CODEC_INT4_SINGLE, n_kv_heads=N_KV), vals))
+    out = torch.empty((N_Q, d_v), dtype=torch.float32, device="cuda")
+    scale = 1.0 / np.sqrt(float(D))
+    f = s.lib.slha_gpu_decode_attention
+    vp = ctypes.c_void_p
+    args_k = [(vp(t.data_ptr()), vp(v.data_ptr()), s.DTYPE_BF16, N_KV, N_TOK, d_v, vp(qc.data_ptr()),
+               vp(qs.data_ptr()), GROUP, ctypes.c_float(scale), vp(out.data_ptr()),
+               vp(stream.cuda_stream)) for t, v in sets]
+    steps, warmup = min(args.steps, 100), min(args.warmup, 10)
+    ms = timed_steps(lambda i: f(*args_k[i % n_sets]), steps, warmup, stream)
+    model.release()
+    nbytes = N_KV * N_TOK * (TILE_BYTES + d_v * 2) + N_Q * (D * 4 + 32) + N_Q * d_v * 4
+    print(json.dumps(line(
+        "decode attention steps/s over compressed keys (32k ctx, 32 heads)", 1.0 / (ms * 1e-3),
+        "steps/s", steps, warmup, ms, "f32",
+        {"workload": "decode attention at the C2 shape (benchmark_decode.rs on the GPU)",
+         "kv_heads": N_KV, "tokens_per_head": N_TOK, "query_heads": N_Q, "group": GROUP,
+         "d_v": d_v, "v_dtype": "bf16", "codec": "int4", "cold_cache_rotation_sets": n_sets,
+         "parallelism": "none (1 GPU)"},
+        roofline=hbm_roofline(nbytes, ms, "score_rows_fast_kernel<4u> + attn_partial_kernel + "
+                              "attn_combine_kernel", "decode"),
+        tokens_attended_per_s=N_Q * N_TOK / (ms * 1e-3))), flush=True)
+    return 0
+
+
 def run_c5(args) -> int:
     """CCOS paged scoring + top-64 over 64 ragged sequences
     in 4096-tile pages shuffled in one arena, 30 % of tiles WARM."""
@@ -411,7 +457,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode"], default="c2",
                     help="c2 (default) is the headline; c3/c4/c5 measure the other "
                          "BASELINE configs at full size")
     args = ap.parse_args()
@@ -424,7 +470,7 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration()
     if args.config != "c2":
-        return {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args)
+        return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode}[args.config](args)
 
     import torch
 

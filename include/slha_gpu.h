@@ -141,6 +141,24 @@ int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_
                                   float* topk_score_dev, void* stream);
 
 /*
+ * Decode attention over compressed keys (the decode step of
+ * scirust/examples/benchmark_decode.rs:29-90): for query head
+ * qh = r*group + j of row r,
+ *   w = softmax(s * scale) over the row's n_tok tiles, s the eq. 2.3 scores
+ *       (SLHA_SCORE_FAST), with softmax_into's contract (metrics.rs:338-409:
+ *       a NaN score or a non-finite scale gives zero weights);
+ *   out_dev[qh][d] = sum_t w_t v_dev[r][t][d]   (aggregate_v, :29-38).
+ * v_dev is [n_rows][n_tok][d_v], f32 or bf16; 1 <= group <= 16; d_v is 32,
+ * 64, 128 or 256. The scores and per-segment partial sums live in a device workspace the
+ * library allocates per (device, stream) on first use and grows as needed
+ * (n_rows*group*(4*n_tok + (d_v+4)*4*ceil(n_tok/512)) bytes).
+ */
+int32_t slha_gpu_decode_attention(const SciRustSlhaTile* tiles_dev, const void* v_dev,
+                                  int32_t v_dtype, size_t n_rows, size_t n_tok, size_t d_v,
+                                  const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                  size_t group, float scale, float* out_dev, void* stream);
+
+/*
  * CCOS ladder steps on device-resident tiles (ccos.rs:369-397), applied to
  * the tiles whose index is listed in slots_dev[n]: op 0 = page_out
  * (HOT->WARM: residual := 0, lambda := 0, |FLAG_WARM), op 1 = drop_correction

@@ -549,6 +549,63 @@ void orc_learned_decode(const float* p, const float* z, size_t d, size_t d_pad, 
     }
 }
 
+/* ---- metrics.rs:338-409 softmax_into; benchmark_decode.rs:29-38 aggregate_v */
+
+void orc_softmax_into(const float* scores, size_t n, float scale, float* out) {
+    if (n == 0) return;
+    if (!isfinite(scale)) {
+        for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return;
+    }
+    const double sc = (double)scale;
+    double maximum = -INFINITY;
+    size_t pos_inf = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const double logit = (double)scores[i] * sc;
+        if (isnan(scores[i]) || isnan(logit)) {
+            for (size_t k = 0; k < n; ++k) out[k] = 0.0f;
+            return;
+        }
+        if (isinf(logit) && logit > 0.0) ++pos_inf;
+        maximum = fmax(maximum, logit);
+    }
+    if (pos_inf > 0) {
+        const float prob = 1.0f / (float)pos_inf;
+        for (size_t i = 0; i < n; ++i) {
+            const double logit = (double)scores[i] * sc;
+            out[i] = (isinf(logit) && logit > 0.0) ? prob : 0.0f;
+        }
+        return;
+    }
+    if (isinf(maximum) && maximum < 0.0) {
+        for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return;
+    }
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        const double e = exp((double)scores[i] * sc - maximum);
+        out[i] = (float)e;
+        sum += e;
+    }
+    if (!isfinite(sum) || sum <= 0.0) {
+        for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return;
+    }
+    for (size_t i = 0; i < n; ++i) out[i] = (float)((double)out[i] / sum);
+    double rounded = 0.0;
+    for (size_t i = 0; i < n; ++i) rounded += (double)out[i];
+    if (isfinite(rounded) && rounded > 0.0)
+        for (size_t i = 0; i < n; ++i) out[i] = (float)((double)out[i] / rounded);
+}
+
+void orc_aggregate_v(const float* weights, const float* values, size_t n, size_t d_v, float* out) {
+    for (size_t j = 0; j < d_v; ++j) out[j] = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float* row = values + i * d_v;
+        for (size_t j = 0; j < d_v; ++j) out[j] += weights[i] * row[j];
+    }
+}
+
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out) {
     for (size_t i = 0; i < n; ++i) {

@@ -122,6 +122,13 @@ int orc_learned_encode(const float* p, const float* z, const float* diag, size_t
 void orc_learned_decode(const float* p, const float* z, size_t d, size_t d_pad, int has_rht,
                         const orc_tile* t, int with_residual, float* out);
 
+/* metrics.rs:338-409 — numerically stable softmax of scores * scale (f64),
+ * with its contract: non-finite scale or a NaN score -> all zero; +inf logits
+ * share the mass equally; all logits -inf -> all zero.
+ * benchmark_decode.rs:29-38 — out[d] = sum_i w_i V[i][d] (f32, in order). */
+void orc_softmax_into(const float* scores, size_t n, float scale, float* out);
+void orc_aggregate_v(const float* weights, const float* values, size_t n, size_t d_v, float* out);
+
 /* Batched helpers for tests (row-major inputs, one tile per key). */
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out);

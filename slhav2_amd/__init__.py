@@ -122,6 +122,8 @@ _SIGS = {
     "slha_gpu_score_paged_topk": (_I32, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P,
                                          _P, _SZ, _P, _P, _P]),
     "slha_gpu_ccos_apply": (_I32, [_P, _P, _SZ, _I32, _P]),
+    "slha_gpu_decode_attention": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _P, _P, _SZ, ctypes.c_float,
+                                         _P, _P]),
     "slha_gpu_synchronize": (_I32, [_P]),
 }
 for _name, (_res, _args) in _SIGS.items():
@@ -413,6 +415,30 @@ def gpu_decode(model: Model, tiles, with_residual: bool = False, stream=None):
     out = torch.empty((t.shape[0], model.dim), dtype=torch.float32, device=t.device)
     _check(lib.slha_gpu_decode(model.handle, _dev_ptr(t), t.shape[0], int(bool(with_residual)),
                                _dev_ptr(out), _stream(stream)))
+    return out
+
+
+def gpu_decode_attention(tiles, values, q_coarse, q_sign, group: int = 1, scale: float | None = None,
+                         out=None, stream=None):
+    """tiles uint8 [n_rows, n_tok, 128], values [n_rows, n_tok, d_v] f32/bf16,
+    q_* [n_rows*group, ...] -> out f32 [n_rows*group, d_v] = softmax(s * scale) V
+    (scale defaults to 1/sqrt(128), benchmark_decode.rs:51)."""
+    import torch
+
+    t = tiles if tiles.dim() == 3 else tiles.unsqueeze(0)
+    v = values if values.dim() == 3 else values.unsqueeze(0)
+    n_rows, n_tok, _ = t.shape
+    d_v = v.shape[2]
+    if v.shape[:2] != (n_rows, n_tok):
+        raise ValueError("values must be [n_rows, n_tok, d_v]")
+    dtype = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}[v.dtype]
+    if scale is None:
+        scale = 1.0 / np.sqrt(128.0)
+    if out is None:
+        out = torch.empty((n_rows * group, d_v), dtype=torch.float32, device=t.device)
+    _check(lib.slha_gpu_decode_attention(_dev_ptr(t), _dev_ptr(v), dtype, n_rows, n_tok, d_v,
+                                         _dev_ptr(q_coarse), _dev_ptr(q_sign), group,
+                                         ctypes.c_float(scale), _dev_ptr(out), _stream(stream)))
     return out
 
 

@@ -1053,6 +1053,42 @@ int32_t slha_gpu_ccos_apply(SciRustSlhaTile* tiles_dev, const uint32_t* slots_de
     });
 }
 
+int32_t slha_gpu_decode_attention(const SciRustSlhaTile* tiles_dev, const void* v_dev,
+                                  int32_t v_dtype, size_t n_rows, size_t n_tok, size_t d_v,
+                                  const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                  size_t group, float scale, float* out_dev, void* stream) {
+    return ffi_status([&] {
+        if (group == 0 || group > 16) fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, 16]", group);
+        if (d_v != 32 && d_v != 64 && d_v != 128 && d_v != 256)
+            fail(SLHA_ERR_DIMENSION, "d_v=%zu must be 32, 64, 128 or 256", d_v);
+        if (v_dtype != SLHA_DTYPE_F32 && v_dtype != SLHA_DTYPE_BF16)
+            fail(SLHA_ERR_DIMENSION, "unknown value dtype %d", v_dtype);
+        if (n_rows > 65535 || n_tok > 0xFFFFFFFFull)
+            fail(SLHA_ERR_DIMENSION, "n_rows=%zu / n_tok=%zu out of range", n_rows, n_tok);
+        if (n_rows == 0) return;
+        if (!out_dev) fail(SLHA_ERR_NULL, "slha_gpu_decode_attention received a NULL pointer");
+        require_device();
+        const hipStream_t hs = static_cast<hipStream_t>(stream);
+        const uint64_t n_out = (uint64_t)n_rows * group * d_v;
+        // softmax_into (metrics.rs:338): a non-finite scale, or no token at
+        // all, gives all-zero weights and so a zero output.
+        if (n_tok == 0 || !std::isfinite(scale)) {
+            check_hip(launch_fill_u32(reinterpret_cast<uint32_t*>(out_dev), n_out, 0u, hs),
+                      "fill kernel");
+            return;
+        }
+        if (!tiles_dev || !v_dev || !q_coarse_dev || !q_sign_dev)
+            fail(SLHA_ERR_NULL, "slha_gpu_decode_attention received a NULL pointer");
+        void* ws = stream_workspace(decode_attention_workspace_bytes((uint32_t)n_rows, (uint32_t)n_tok,
+                                                                     (uint32_t)group, (uint32_t)d_v),
+                                    hs);
+        check_hip(launch_decode_attention(tiles_dev, v_dev, v_dtype, (uint32_t)n_rows,
+                                          (uint32_t)n_tok, (uint32_t)group, (uint32_t)d_v,
+                                          q_coarse_dev, q_sign_dev, scale, out_dev, ws, hs),
+                  "decode attention kernels");
+    });
+}
+
 int32_t slha_gpu_synchronize(void* stream) {
     return ffi_status([&] {
         require_device();

@@ -2489,6 +2489,191 @@ __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __rest
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention over compressed keys (benchmark_decode.rs:29-90): for
+// query head qh = r*group + j of row r,
+//     w = softmax(scores[qh] * scale)      (metrics.rs:338, softmax_into)
+//     out[qh][d] = sum_t w_t V[r][t][d]     (aggregate_v, benchmark_decode.rs:29-38)
+// with the scores of slha_gpu_score (fast mode). Split over tokens as in
+// flash decoding: attn_partial_kernel turns each segment of kAttnSeg tokens
+// of a row into (max m, sum l of exp(logit - m), o = sum exp(logit - m) V)
+// for every query of the row, reading each V row once for the whole group;
+// attn_combine_kernel merges the segments: out = sum_s e^(m_s - M) o_s /
+// sum_s e^(m_s - M) l_s. A NaN score, as in softmax_into, zeroes the query's
+// output; scores of valid tiles against prepared (finite) queries are
+// finite, so the other degenerate cases of softmax_into (+inf logits, all
+// logits -inf) do not arise here.
+constexpr uint32_t kAttnSeg = 256;  // tokens per partial block (one per thread in phase 1)
+constexpr uint32_t kAttnMaxGroup = 16;
+
+__host__ __device__ constexpr size_t attn_partial_floats(uint32_t d_v) { return (size_t)d_v + 4; }
+
+// Max (or sum) over the 256 threads of each of G values, in place: xor
+// shuffles within each wave, then the 4 wave results through LDS.
+template <int G, bool MAX>
+__device__ __forceinline__ void block_reduce_g(float* x, float (*tmp)[4]) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const float y = __shfl_xor(x[j], o);
+            x[j] = MAX ? fmaxf(x[j], y) : x[j] + y;
+        }
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0)
+#pragma unroll
+        for (int j = 0; j < G; ++j) tmp[j][threadIdx.x >> 6] = x[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+        x[j] = MAX ? fmaxf(fmaxf(tmp[j][0], tmp[j][1]), fmaxf(tmp[j][2], tmp[j][3]))
+                   : (tmp[j][0] + tmp[j][1]) + (tmp[j][2] + tmp[j][3]);
+}
+
+// grid (n_seg, n_rows), 256 threads; group <= G (a power of two <=
+// kAttnMaxGroup), VDT the V element type, DV = d_v.
+// part[((r * n_seg + seg) * group + j)] = {m, l, -, -, o[DV]} (l = NaN when a
+// score of the segment is NaN).
+//  phase 1: thread t holds token t0 + t: logits, per-query max and sum of
+//           exp(logit - max) over the segment, weights e[j][t] in LDS;
+//  phase 2: lane group of LPT = DV / VEC lanes reads one token's V row as
+//           16-byte vectors (VEC elements per lane), TPS = 256 / LPT tokens
+//           per step; each lane accumulates G x VEC outputs, then the TPS
+//           token slots are summed (xor shuffles inside the wave, LDS across
+//           the waves).
+template <int VDT, int G, int DV>
+__global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ scores,
+                                                           const void* __restrict__ vals,
+                                                           uint32_t n_tok, uint32_t group,
+                                                           float scale, float* __restrict__ part) {
+    constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;  // V elements per 16-byte lane load
+    constexpr int LPT = DV / VEC;                   // lanes per token row
+    constexpr int TPW = 64 / LPT;                   // tokens per wave step
+    constexpr int TPS = 4 * TPW;                    // tokens per block step
+    __shared__ float e[G][kAttnSeg];
+    __shared__ float tmp[G][4];
+    __shared__ float red[4][G][DV];
+    const uint32_t seg = blockIdx.x, row = blockIdx.y, n_seg = gridDim.x;
+    const uint32_t t0 = seg * kAttnSeg;
+    const uint32_t nt = n_tok - t0 < kAttnSeg ? n_tok - t0 : kAttnSeg;
+    const uint32_t tid = threadIdx.x;
+    // phase 1
+    float lg[G], m[G], l[G], nan[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        lg[j] = -INFINITY;
+        nan[j] = 0.0f;
+        if (tid < nt && (uint32_t)j < group) {
+            const float sc = scores[((size_t)row * group + j) * n_tok + t0 + tid];
+            nan[j] = isnan(sc) ? 1.0f : 0.0f;
+            lg[j] = sc * scale;
+        }
+        m[j] = lg[j];
+    }
+    block_reduce_g<G, true>(m, tmp);
+    block_reduce_g<G, true>(nan, tmp);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const float w = tid < nt ? __expf(lg[j] - m[j]) : 0.0f;
+        e[j][tid] = w;
+        l[j] = w;
+    }
+    block_reduce_g<G, false>(l, tmp);  // its barriers also publish e
+    // phase 2
+    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    const uint32_t slot = wave * TPW + lane / LPT;  // token slot 0 .. TPS-1
+    const uint32_t dc = lane % LPT;                 // this lane's VEC dims: dc*VEC ..
+    float o[G][VEC];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
+    const char* vrow = static_cast<const char*>(vals) +
+                       (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
+    constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
+#pragma unroll 4
+    for (uint32_t tb = 0; tb < kAttnSeg; tb += TPS) {
+        const uint32_t t = tb + slot;
+        if (t < nt) {
+            const uint4 x = *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
+            float v[VEC];
+            if constexpr (VDT == kDtypeBF16) {
+                const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[2 * k] = __uint_as_float(u[k] << 16);
+                    v[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+                }
+            } else {
+                v[0] = __uint_as_float(x.x), v[1] = __uint_as_float(x.y);
+                v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
+            }
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const float w = e[j][t];
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(w, v[k], o[j][k]);
+            }
+        }
+    }
+    // sum over the TPW token slots of the wave (lanes lane % LPT equal) ...
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1)
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) o[j][k] += __shfl_xor(o[j][k], off);
+    // ... then over the 4 waves
+    if (lane < LPT)
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) red[wave][j][dc * VEC + k] = o[j][k];
+    __syncthreads();
+    for (uint32_t i = tid; i < group * DV; i += 256u) {
+        const uint32_t j = i / DV, d = i % DV;
+        float* pp = part + (((size_t)row * n_seg + seg) * group + j) * attn_partial_floats(DV);
+        pp[4 + d] = (red[0][j][d] + red[1][j][d]) + (red[2][j][d] + red[3][j][d]);
+        if (d == 0) pp[0] = m[j], pp[1] = nan[j] != 0.0f ? NAN : l[j];
+    }
+}
+
+// grid (n_rows * group, ceil(d_v / 64)), 256 threads: wave w merges segments
+// w, w + 4, ... for the 64 dims of its block; LDS adds the 4 waves.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
+                                                           uint32_t n_seg, uint32_t group,
+                                                           uint32_t d_v, float* __restrict__ out) {
+    __shared__ float acc_w[4][64], l_w[4];
+    __shared__ uint32_t nan_w[4];
+    const uint32_t qh = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t d = blockIdx.y * 64u + lane;
+    const uint32_t row = qh / group, j = qh % group;
+    const size_t stride = (size_t)group * attn_partial_floats(d_v);  // one segment
+    const float* p0 = part + ((size_t)row * n_seg * group + j) * attn_partial_floats(d_v);
+    float M = -INFINITY;
+    for (uint32_t s = lane; s < n_seg; s += 64u) M = fmaxf(M, p0[s * stride]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.0f, acc = 0.0f;
+    bool nan = false;
+    for (uint32_t s = wave; s < n_seg; s += 4u) {
+        const float* ps = p0 + s * stride;
+        const float f = __expf(ps[0] - M);
+        nan = nan || isnan(ps[1]);
+        L = fmaf(ps[1], f, L);
+        if (d < d_v) acc = fmaf(ps[4 + d], f, acc);
+    }
+    acc_w[wave][lane] = acc;
+    if (lane == 0) l_w[wave] = L, nan_w[wave] = nan ? 1u : 0u;
+    __syncthreads();
+    if (wave == 0 && d < d_v) {
+        const float Lt = (l_w[0] + l_w[1]) + (l_w[2] + l_w[3]);
+        const float At = (acc_w[0][lane] + acc_w[1][lane]) + (acc_w[2][lane] + acc_w[3][lane]);
+        const bool bad = (nan_w[0] | nan_w[1] | nan_w[2] | nan_w[3]) != 0u || !(Lt > 0.0f);
+        out[(size_t)qh * d_v + d] = bad ? 0.0f : At / Lt;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Launchers
 
 size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
@@ -2737,6 +2922,72 @@ hipError_t launch_learned_decode(const void* tiles, uint64_t n, const LearnedPro
     return hipGetLastError();
 }
 
+namespace {
+template <int VDT, int G>
+hipError_t attn_partial_dv(dim3 grid, const float* scores, const void* vals, uint32_t n_tok,
+                           uint32_t group, uint32_t d_v, float scale, float* part, hipStream_t s) {
+#define SLHA_DV(DV)                                                                              \
+    case DV:                                                                                     \
+        attn_partial_kernel<VDT, G, DV><<<grid, 256, 0, s>>>(scores, vals, n_tok, group, scale, part); \
+        break;
+    switch (d_v) {
+        SLHA_DV(32) SLHA_DV(64) SLHA_DV(128) SLHA_DV(256)
+        default: return hipErrorInvalidValue;
+    }
+#undef SLHA_DV
+    return hipGetLastError();
+}
+template <int VDT>
+hipError_t attn_partial_g(dim3 grid, const float* scores, const void* vals, uint32_t n_tok,
+                          uint32_t group, uint32_t d_v, float scale, float* part, hipStream_t s) {
+    if (group <= 1) return attn_partial_dv<VDT, 1>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+    if (group <= 2) return attn_partial_dv<VDT, 2>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+    if (group <= 4) return attn_partial_dv<VDT, 4>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+    if (group <= 8) return attn_partial_dv<VDT, 8>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+    return attn_partial_dv<VDT, 16>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+}
+hipError_t attn_partial_dispatch(dim3 grid, const float* scores, const void* vals, int v_dtype,
+                                 uint32_t n_tok, uint32_t group, uint32_t d_v, float scale,
+                                 float* part, hipStream_t s) {
+    return v_dtype == kDtypeBF16
+               ? attn_partial_g<kDtypeBF16>(grid, scores, vals, n_tok, group, d_v, scale, part, s)
+               : attn_partial_g<kDtypeF32>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+}
+}  // namespace
+
+size_t decode_attention_workspace_bytes(uint32_t n_rows, uint32_t n_tok, uint32_t group,
+                                        uint32_t d_v) {
+    const size_t n_seg = (n_tok + kAttnSeg - 1) / kAttnSeg;
+    const size_t scores = (size_t)n_rows * group * n_tok * 4;
+    const size_t part = (size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4;
+    const size_t wide = score_rows_workspace_bytes(n_rows, group, false, false);
+    return ((scores + 255) & ~(size_t)255) + ((part + 255) & ~(size_t)255) + wide;
+}
+
+hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dtype,
+                                   uint32_t n_rows, uint32_t n_tok, uint32_t group, uint32_t d_v,
+                                   const float* qc, const uint64_t* qs, float scale, float* out,
+                                   void* workspace, hipStream_t s) {
+    if (n_rows == 0 || n_tok == 0 || group == 0) return hipSuccess;
+    if (group > kAttnMaxGroup || d_v < 32 || d_v > 256 || (d_v & (d_v - 1)) != 0)
+        return hipErrorInvalidValue;
+    const uint32_t n_seg = (n_tok + kAttnSeg - 1) / kAttnSeg;
+    char* ws = static_cast<char*>(workspace);
+    float* scores = reinterpret_cast<float*>(ws);
+    const size_t sb = ((size_t)n_rows * group * n_tok * 4 + 255) & ~(size_t)255;
+    float* part = reinterpret_cast<float*>(ws + sb);
+    const size_t pb = ((size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4 + 255) & ~(size_t)255;
+    hipError_t e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr,
+                                     ws + sb + pb, s);
+    if (e != hipSuccess) return e;
+    const dim3 grid(n_seg, n_rows);
+    e = attn_partial_dispatch(grid, scores, vals, v_dtype, n_tok, group, d_v, scale, part, s);
+    if (e != hipSuccess) return e;
+    attn_combine_kernel<<<dim3(n_rows * group, (d_v + 63) / 64), 256, 0, s>>>(part, n_seg, group, d_v,
+                                                                            out);
+    return hipGetLastError();
+}
+
 hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s) {
     if (n == 0) return hipSuccess;
     validate_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
@@ -2752,6 +3003,17 @@ __global__ void fill_u64_kernel(uint64_t* p, uint64_t n, uint64_t value) {
 hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s) {
     if (n == 0) return hipSuccess;
     fill_u64_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, value);
+    return hipGetLastError();
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t value) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = value;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t value, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, value);
     return hipGetLastError();
 }
 

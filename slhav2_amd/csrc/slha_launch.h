@@ -79,10 +79,21 @@ hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const 
 // estimate when the model has no RHT).
 hipError_t launch_learned_decode(const void* tiles, uint64_t n, const LearnedProjection& lp,
                                  int with_residual, float sqrt_half_pi, float* out, hipStream_t s);
+// Decode attention over compressed keys: scores (fast mode), softmax of
+// scores * scale, out[qh][d_v] = sum_t w_t V[row][t][:]. V is [n_rows][n_tok][d_v]
+// (f32 or bf16), group <= 16, d_v is 32, 64, 128 or 256. `workspace` holds
+// decode_attention_workspace_bytes().
+hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dtype,
+                                   uint32_t n_rows, uint32_t n_tok, uint32_t group, uint32_t d_v,
+                                   const float* qc, const uint64_t* qs, float scale, float* out,
+                                   void* workspace, hipStream_t s);
+size_t decode_attention_workspace_bytes(uint32_t n_rows, uint32_t n_tok, uint32_t group,
+                                        uint32_t d_v);
 hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, float sqrt_half_pi,
                          float* out, hipStream_t s);
 hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s);
 hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t value, hipStream_t s);
 
 }  // namespace slha

@@ -86,6 +86,8 @@ for name, res, args in [
     ("orc_learned_encode", ctypes.c_int, [_P, _P, _P, _SZ, _SZ, _P, ctypes.c_uint32, ctypes.c_int,
                                           ctypes.c_int, _P]),
     ("orc_learned_decode", None, [_P, _P, _SZ, _SZ, ctypes.c_int, _P, ctypes.c_int, _P]),
+    ("orc_softmax_into", None, [_P, _SZ, _F, _P]),
+    ("orc_aggregate_v", None, [_P, _P, _SZ, _SZ, _P]),
 ]:
     fn = getattr(lib, name)
     fn.restype = res
@@ -312,3 +314,27 @@ class Learned:
                                    int(self.diag is not None), t[i:i + 1].ctypes.data,
                                    int(with_residual), out[i].ctypes.data)
         return out
+
+
+def softmax(scores, scale: float) -> np.ndarray:
+    """metrics.rs:338-409 softmax_into."""
+    sc = f32(scores)
+    out = np.zeros(len(sc), np.float32)
+    lib.orc_softmax_into(_p(sc), len(sc), scale, _p(out))
+    return out
+
+
+def aggregate(weights, values) -> np.ndarray:
+    """benchmark_decode.rs:29-38 aggregate_v: weights [n], values [n, d_v]."""
+    w = f32(weights)
+    v = f32(values)
+    out = np.zeros(v.shape[1], np.float32)
+    lib.orc_aggregate_v(_p(w), _p(v), len(w), v.shape[1], _p(out))
+    return out
+
+
+def decode_attention(tiles, values, q_coarse, q_sign, scale: float) -> np.ndarray:
+    """One query head's decode step over one row: exact eq. 2.3 scores,
+    softmax_into, aggregate_v (benchmark_decode.rs:84-90)."""
+    sc, _ = score(tiles, q_coarse, q_sign)
+    return aggregate(softmax(sc, scale), values)
