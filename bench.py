@@ -367,8 +367,7 @@ def run_decode(args) -> int:
          "kv_heads": N_KV, "tokens_per_head": N_TOK, "query_heads": N_Q, "group": GROUP,
          "d_v": d_v, "v_dtype": "bf16", "codec": "int4", "cold_cache_rotation_sets": n_sets,
          "parallelism": "none (1 GPU)"},
-        roofline=hbm_roofline(nbytes, ms, "score_rows_fast_kernel<4u> + attn_partial_kernel + "
-                              "attn_combine_kernel", "decode"),
+        roofline=hbm_roofline(nbytes, ms, "attn_fused_kernel + attn_combine_kernel", "decode"),
         tokens_attended_per_s=N_Q * N_TOK / (ms * 1e-3))), flush=True)
     return 0
 

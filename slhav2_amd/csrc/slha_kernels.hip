@@ -2556,6 +2556,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     const uint32_t t0 = seg * kAttnSeg;
     const uint32_t nt = n_tok - t0 < kAttnSeg ? n_tok - t0 : kAttnSeg;
     const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    const uint32_t slot = wave * TPW + lane / LPT;  // token slot 0 .. TPS-1
+    const uint32_t dc = lane % LPT;                 // this lane's VEC dims: dc*VEC ..
+    const char* vrow = static_cast<const char*>(vals) +
+                       (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
+    constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
+    // The first kPre V vectors of this thread are loaded before the softmax
+    // reductions, so their latency overlaps the block's barriers.
+    constexpr uint32_t kSteps = kAttnSeg / TPS, kPre = kSteps < 8 ? kSteps : 8;
+    uint4 pre[kPre];
+#pragma unroll
+    for (uint32_t k = 0; k < kPre; ++k) {
+        const uint32_t t = k * TPS + slot;
+        pre[k] = t < nt ? *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes)
+                        : make_uint4(0u, 0u, 0u, 0u);
+    }
     // phase 1
     float lg[G], m[G], l[G], nan[G];
 #pragma unroll
@@ -2579,22 +2595,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     }
     block_reduce_g<G, false>(l, tmp);  // its barriers also publish e
     // phase 2
-    const uint32_t wave = tid >> 6, lane = tid & 63u;
-    const uint32_t slot = wave * TPW + lane / LPT;  // token slot 0 .. TPS-1
-    const uint32_t dc = lane % LPT;                 // this lane's VEC dims: dc*VEC ..
     float o[G][VEC];
 #pragma unroll
     for (int j = 0; j < G; ++j)
 #pragma unroll
         for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
-    const char* vrow = static_cast<const char*>(vals) +
-                       (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
-    constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
-#pragma unroll 4
-    for (uint32_t tb = 0; tb < kAttnSeg; tb += TPS) {
-        const uint32_t t = tb + slot;
+#pragma unroll
+    for (uint32_t step = 0; step < kSteps; ++step) {
+        const uint32_t t = step * TPS + slot;
         if (t < nt) {
-            const uint4 x = *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
+            const uint4 x = step < kPre ? pre[step < kPre ? step : 0]
+                                        : *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
             float v[VEC];
             if constexpr (VDT == kDtypeBF16) {
                 const uint32_t u[4] = {x.x, x.y, x.z, x.w};
@@ -2637,38 +2648,200 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     }
 }
 
-// grid (n_rows * group, ceil(d_v / 64)), 256 threads: wave w merges segments
-// w, w + 4, ... for the 64 dims of its block; LDS adds the 4 waves.
+// Fused segment kernel for group <= 4: the 256 tokens of the segment are
+// scored exactly as score_rows_fast_kernel<4> scores them (same tile DMA,
+// query staging and MFMA paths), into LDS instead of HBM, and the block then
+// runs the softmax and softmax.V phases of attn_partial_kernel on them. The
+// first V vectors are issued before the tile fetch so both streams overlap.
+template <int VDT, int DV>
+__global__ __launch_bounds__(256) void attn_fused_kernel(const uint4* __restrict__ tiles,
+                                                         uint32_t n_tok, uint32_t group,
+                                                         const float* __restrict__ qc,
+                                                         const uint32_t* __restrict__ qs,
+                                                         const void* __restrict__ vals, float scale,
+                                                         float* __restrict__ part) {
+    constexpr int G = 4;
+    constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;
+    constexpr int LPT = DV / VEC, TPW = 64 / LPT, TPS = 4 * TPW;
+    constexpr uint32_t kSteps = kAttnSeg / TPS, kPre = kSteps < 8 ? kSteps : 8;
+    constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
+    __shared__ float cb[16];
+    __shared__ uint4 tile_lds[4][512];
+    __shared__ __attribute__((aligned(16))) float qstatic[staging_bytes(4) / 4];
+    __shared__ float e[G][kAttnSeg];  // scores, then weights
+    __shared__ float tmp[G][4];
+    __shared__ float red[4][G][DV];
+    const uint32_t seg = blockIdx.x, row = blockIdx.y, n_seg = gridDim.x;
+    const uint32_t t0 = seg * kAttnSeg;
+    const uint32_t nt = n_tok - t0 < kAttnSeg ? n_tok - t0 : kAttnSeg;
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
+    const size_t qrow0 = (size_t)row * group;
+    // V prefetch
+    const uint32_t slot = wave * TPW + lane / LPT, dc = lane % LPT;
+    const char* vrow = static_cast<const char*>(vals) +
+                       (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
+    uint4 pre[kPre];
+#pragma unroll
+    for (uint32_t k = 0; k < kPre; ++k) {
+        const uint32_t t = k * TPS + slot;
+        pre[k] = t < nt ? *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes)
+                        : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // Scores of the segment (score_rows_fast_kernel<4>), into e[j][t].
+    {
+        const StagedQueries sq = carve_staging(qstatic, 4);
+        QueryRegs<4> qr;
+        stage_issue<4>(qc, qrow0, group, qr);
+        const uint32_t wave0 = t0 + 64u * wave;
+        const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+        fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+        stage_codebook(cb);
+        stage_commit<4>(qr, group, sq);
+        lds_barrier();
+        uint32_t w[32];
+        fetch_tiles_readback(tile_lds[wave], w);
+        const uint32_t tl = 64u * wave + lane;
+        const bool valid = t0 + tl < n_tok;
+        float* out = &e[0][0];
+        if (!score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out,
+                                 kAttnSeg, tl) &&
+            valid)
+            score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, kAttnSeg, tl);
+    }
+    __syncthreads();
+    // Softmax statistics (thread t holds token t).
+    float lg[G], m[G], l[G], nan[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        lg[j] = -INFINITY;
+        nan[j] = 0.0f;
+        if (tid < nt && (uint32_t)j < group) {
+            const float sc = e[j][tid];
+            nan[j] = isnan(sc) ? 1.0f : 0.0f;
+            lg[j] = sc * scale;
+        }
+        m[j] = lg[j];
+    }
+    block_reduce_g<G, true>(m, tmp);
+    block_reduce_g<G, true>(nan, tmp);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const float wgt = tid < nt ? __expf(lg[j] - m[j]) : 0.0f;
+        e[j][tid] = wgt;
+        l[j] = wgt;
+    }
+    block_reduce_g<G, false>(l, tmp);
+    // softmax.V
+    float o[G][VEC];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
+#pragma unroll
+    for (uint32_t step = 0; step < kSteps; ++step) {
+        const uint32_t t = step * TPS + slot;
+        if (t < nt) {
+            const uint4 x = step < kPre ? pre[step < kPre ? step : 0]
+                                        : *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
+            float v[VEC];
+            if constexpr (VDT == kDtypeBF16) {
+                const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[2 * k] = __uint_as_float(u[k] << 16);
+                    v[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+                }
+            } else {
+                v[0] = __uint_as_float(x.x), v[1] = __uint_as_float(x.y);
+                v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
+            }
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const float wgt = e[j][t];
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(wgt, v[k], o[j][k]);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1)
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) o[j][k] += __shfl_xor(o[j][k], off);
+    if (lane < LPT)
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) red[wave][j][dc * VEC + k] = o[j][k];
+    __syncthreads();
+    for (uint32_t i = tid; i < group * DV; i += 256u) {
+        const uint32_t j = i / DV, d = i % DV;
+        float* pp = part + (((size_t)row * n_seg + seg) * group + j) * attn_partial_floats(DV);
+        pp[4 + d] = (red[0][j][d] + red[1][j][d]) + (red[2][j][d] + red[3][j][d]);
+        if (d == 0) pp[0] = m[j], pp[1] = nan[j] != 0.0f ? NAN : l[j];
+    }
+}
+
+// grid (n_rows * group, d_v / 16), 256 threads: thread (sl, c) = (tid / 16,
+// tid % 16) merges segments sl, sl + 16, ... for dim 16 blockIdx.y + c; the
+// 16 segment lanes are then added (xor shuffles, then LDS across waves).
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
                                                            uint32_t n_seg, uint32_t group,
                                                            uint32_t d_v, float* __restrict__ out) {
-    __shared__ float acc_w[4][64], l_w[4];
-    __shared__ uint32_t nan_w[4];
-    const uint32_t qh = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t d = blockIdx.y * 64u + lane;
+    __shared__ float red_a[4][16], red_l[4], red_m[4];
+    __shared__ uint32_t red_n[4];
+    const uint32_t qh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t c = tid & 15u, sl = tid >> 4;
+    const uint32_t d = blockIdx.y * 16u + c;
     const uint32_t row = qh / group, j = qh % group;
     const size_t stride = (size_t)group * attn_partial_floats(d_v);  // one segment
     const float* p0 = part + ((size_t)row * n_seg * group + j) * attn_partial_floats(d_v);
     float M = -INFINITY;
-    for (uint32_t s = lane; s < n_seg; s += 64u) M = fmaxf(M, p0[s * stride]);
+#pragma unroll 8
+    for (uint32_t s = sl; s < n_seg; s += 16u) M = fmaxf(M, p0[s * stride]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    float L = 0.0f, acc = 0.0f;
-    bool nan = false;
-    for (uint32_t s = wave; s < n_seg; s += 4u) {
-        const float* ps = p0 + s * stride;
-        const float f = __expf(ps[0] - M);
-        nan = nan || isnan(ps[1]);
-        L = fmaf(ps[1], f, L);
-        if (d < d_v) acc = fmaf(ps[4 + d], f, acc);
-    }
-    acc_w[wave][lane] = acc;
-    if (lane == 0) l_w[wave] = L, nan_w[wave] = nan ? 1u : 0u;
+    if ((tid & 63u) == 0) red_m[wave] = M;
     __syncthreads();
-    if (wave == 0 && d < d_v) {
-        const float Lt = (l_w[0] + l_w[1]) + (l_w[2] + l_w[3]);
-        const float At = (acc_w[0][lane] + acc_w[1][lane]) + (acc_w[2][lane] + acc_w[3][lane]);
-        const bool bad = (nan_w[0] | nan_w[1] | nan_w[2] | nan_w[3]) != 0u || !(Lt > 0.0f);
+    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    // Eight segments per step with independent accumulators: their loads are
+    // in flight together.
+    constexpr uint32_t U = 8;
+    float Lu[U], Au[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) Lu[u] = 0.0f, Au[u] = 0.0f;
+    bool nan = false;
+    for (uint32_t s0 = sl; s0 < n_seg; s0 += 16u * U) {
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t s = s0 + 16u * u;
+            if (s < n_seg) {
+                const float* ps = p0 + s * stride;
+                const float f = __expf(ps[0] - M);
+                nan = nan || isnan(ps[1]);
+                Lu[u] = fmaf(ps[1], f, Lu[u]);
+                Au[u] = fmaf(ps[4 + d], f, Au[u]);
+            }
+        }
+    }
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) L += Lu[u], acc += Au[u];
+    uint32_t nn = nan ? 1u : 0u;
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {  // the 4 segment lanes of this wave
+        L += __shfl_xor(L, o);
+        acc += __shfl_xor(acc, o);
+        nn |= (uint32_t)__shfl_xor((int)nn, o);
+    }
+    if ((tid & 63u) < 16u) red_a[wave][c] = acc;
+    if ((tid & 63u) == 0) red_l[wave] = L, red_n[wave] = nn;
+    __syncthreads();
+    if (tid < 16u) {
+        const float Lt = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
+        const float At = (red_a[0][c] + red_a[1][c]) + (red_a[2][c] + red_a[3][c]);
+        const bool bad = (red_n[0] | red_n[1] | red_n[2] | red_n[3]) != 0u || !(Lt > 0.0f);
         out[(size_t)qh * d_v + d] = bad ? 0.0f : At / Lt;
     }
 }
@@ -2977,14 +3150,36 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
     const size_t sb = ((size_t)n_rows * group * n_tok * 4 + 255) & ~(size_t)255;
     float* part = reinterpret_cast<float*>(ws + sb);
     const size_t pb = ((size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4 + 255) & ~(size_t)255;
-    hipError_t e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr,
-                                     ws + sb + pb, s);
+    const uint4* tp = static_cast<const uint4*>(tiles);
+    const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
+    hipError_t e = hipSuccess;
+    if (group <= 4) {  // scores stay in LDS
+        const dim3 grid(n_seg, n_rows);
+#define SLHA_FUSED(VDT, DV)                                                                         \
+    attn_fused_kernel<VDT, DV><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part)
+        switch ((v_dtype == kDtypeBF16 ? 1000 : 0) + (int)d_v) {
+            case 32: SLHA_FUSED(kDtypeF32, 32); break;
+            case 64: SLHA_FUSED(kDtypeF32, 64); break;
+            case 128: SLHA_FUSED(kDtypeF32, 128); break;
+            case 256: SLHA_FUSED(kDtypeF32, 256); break;
+            case 1032: SLHA_FUSED(kDtypeBF16, 32); break;
+            case 1064: SLHA_FUSED(kDtypeBF16, 64); break;
+            case 1128: SLHA_FUSED(kDtypeBF16, 128); break;
+            case 1256: SLHA_FUSED(kDtypeBF16, 256); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef SLHA_FUSED
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, out);
+        return hipGetLastError();
+    }
+    e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr, ws + sb + pb, s);
     if (e != hipSuccess) return e;
     const dim3 grid(n_seg, n_rows);
     e = attn_partial_dispatch(grid, scores, vals, v_dtype, n_tok, group, d_v, scale, part, s);
     if (e != hipSuccess) return e;
-    attn_combine_kernel<<<dim3(n_rows * group, (d_v + 63) / 64), 256, 0, s>>>(part, n_seg, group, d_v,
-                                                                            out);
+    attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, out);
     return hipGetLastError();
 }
 
