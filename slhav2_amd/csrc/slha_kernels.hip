@@ -2648,90 +2648,86 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     }
 }
 
-// Fused segment kernel for group <= 4: the 256 tokens of the segment are
-// scored exactly as score_rows_fast_kernel<4> scores them (same tile DMA,
-// query staging and MFMA paths), into LDS instead of HBM, and the block then
-// runs the softmax and softmax.V phases of attn_partial_kernel on them. The
-// first V vectors are issued before the tile fetch so both streams overlap.
+// Fused segment kernel for group <= 4, grid (n_seg, n_rows), 256 threads.
+// Wave w scores tokens t0 + 64 w .. +63 exactly as score_rows_fast_kernel<4>
+// scores them (same tile DMA, query staging and MFMA paths) and runs a
+// flash-decoding step over its own 64 tokens: wave max m_w, weights
+// exp(logit - m_w), sum l_w and o_w = sum weight * V. The block merges its four
+// waves with exp(m_w - M) into one partial {M, L, -, -, O[DV]} (L = NaN when a
+// score of the segment is NaN), read by attn_combine_kernel. Once a wave has
+// read its tiles back, its 8 KiB tile region holds its weights [G][64] and
+// then its o_w [G][DV], so the block needs about 37 KiB of LDS and, at <= 128
+// VGPRs, four blocks share a CU: the decode grid (128 x 8) is resident at once.
 template <int VDT, int DV>
-__global__ __launch_bounds__(256) void attn_fused_kernel(const uint4* __restrict__ tiles,
-                                                         uint32_t n_tok, uint32_t group,
-                                                         const float* __restrict__ qc,
-                                                         const uint32_t* __restrict__ qs,
-                                                         const void* __restrict__ vals, float scale,
-                                                         float* __restrict__ part) {
+__global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restrict__ tiles,
+                                                            uint32_t n_tok, uint32_t group,
+                                                            const float* __restrict__ qc,
+                                                            const uint32_t* __restrict__ qs,
+                                                            const void* __restrict__ vals,
+                                                            float scale, float* __restrict__ part) {
     constexpr int G = 4;
-    constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;
-    constexpr int LPT = DV / VEC, TPW = 64 / LPT, TPS = 4 * TPW;
-    constexpr uint32_t kSteps = kAttnSeg / TPS, kPre = kSteps < 8 ? kSteps : 8;
+    constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;  // V elements per 16-byte load
+    constexpr int LPT = DV / VEC, TPW = 64 / LPT;   // lanes per token, tokens per wave step
+    constexpr uint32_t kSteps = 64 / TPW;
     constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
+    static_assert(G * (64 + DV) * 4 <= 512 * 16, "weights and o_w fit the tile region");
     __shared__ float cb[16];
     __shared__ uint4 tile_lds[4][512];
     __shared__ __attribute__((aligned(16))) float qstatic[staging_bytes(4) / 4];
-    __shared__ float e[G][kAttnSeg];  // scores, then weights
-    __shared__ float tmp[G][4];
-    __shared__ float red[4][G][DV];
+    __shared__ float wst[4][G][3];  // per wave: m_w, l_w, NaN seen
     const uint32_t seg = blockIdx.x, row = blockIdx.y, n_seg = gridDim.x;
-    const uint32_t t0 = seg * kAttnSeg;
-    const uint32_t nt = n_tok - t0 < kAttnSeg ? n_tok - t0 : kAttnSeg;
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
     const size_t qrow0 = (size_t)row * group;
-    // V prefetch
-    const uint32_t slot = wave * TPW + lane / LPT, dc = lane % LPT;
-    const char* vrow = static_cast<const char*>(vals) +
-                       (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
-    uint4 pre[kPre];
-#pragma unroll
-    for (uint32_t k = 0; k < kPre; ++k) {
-        const uint32_t t = k * TPS + slot;
-        pre[k] = t < nt ? *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes)
-                        : make_uint4(0u, 0u, 0u, 0u);
-    }
-    // Scores of the segment (score_rows_fast_kernel<4>), into e[j][t].
+    const uint32_t wave0 = seg * kAttnSeg + 64u * wave;
+    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    const uint32_t nw = n_valid < 64u ? n_valid : 64u;  // tokens of this wave
+    float* ew = reinterpret_cast<float*>(tile_lds[wave]);  // [G][64] after the readback
+    float* ow = ew + G * 64;                               // [G][DV]
     {
         const StagedQueries sq = carve_staging(qstatic, 4);
         QueryRegs<4> qr;
         stage_issue<4>(qc, qrow0, group, qr);
-        const uint32_t wave0 = t0 + 64u * wave;
-        const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
         fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
         stage_codebook(cb);
         stage_commit<4>(qr, group, sq);
         lds_barrier();
         uint32_t w[32];
         fetch_tiles_readback(tile_lds[wave], w);
-        const uint32_t tl = 64u * wave + lane;
-        const bool valid = t0 + tl < n_tok;
-        float* out = &e[0][0];
-        if (!score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out,
-                                 kAttnSeg, tl) &&
+        const bool valid = lane < nw;
+        if (!score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, ew, 64,
+                                 lane) &&
             valid)
-            score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, kAttnSeg, tl);
+            score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, ew, nullptr, 64, lane);
     }
-    __syncthreads();
-    // Softmax statistics (thread t holds token t).
-    float lg[G], m[G], l[G], nan[G];
+    // Softmax statistics of the wave; lane holds token wave0 + lane.
+    float m[G], l[G];
+    bool bad[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-        lg[j] = -INFINITY;
-        nan[j] = 0.0f;
-        if (tid < nt && (uint32_t)j < group) {
-            const float sc = e[j][tid];
-            nan[j] = isnan(sc) ? 1.0f : 0.0f;
-            lg[j] = sc * scale;
+        float lg = -INFINITY;
+        bool nan_j = false;
+        if (lane < nw && (uint32_t)j < group) {
+            const float sc = ew[j * 64 + lane];
+            nan_j = isnan(sc);
+            lg = sc * scale;
         }
-        m[j] = lg[j];
-    }
-    block_reduce_g<G, true>(m, tmp);
-    block_reduce_g<G, true>(nan, tmp);
+        bad[j] = __any(nan_j);
+        float mx = lg;
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        const float wgt = tid < nt ? __expf(lg[j] - m[j]) : 0.0f;
-        e[j][tid] = wgt;
-        l[j] = wgt;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        m[j] = mx;
+        const float wgt = lane < nw ? __expf(lg - mx) : 0.0f;
+        ew[j * 64 + lane] = wgt;
+        float sm = wgt;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sm += __shfl_xor(sm, o);
+        l[j] = sm;
     }
-    block_reduce_g<G, false>(l, tmp);
-    // softmax.V
+    // o_w: lane group slot = lane / LPT reads token slot + TPW * step, dims
+    // dc * VEC .. +VEC-1, with one 16-byte load.
+    const uint32_t slot = lane / LPT, dc = lane % LPT;
+    const char* vrow = static_cast<const char*>(vals) +
+                       (((size_t)row * n_tok + wave0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
     float o[G][VEC];
 #pragma unroll
     for (int j = 0; j < G; ++j)
@@ -2739,10 +2735,9 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const uint4* __restrict
         for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
 #pragma unroll
     for (uint32_t step = 0; step < kSteps; ++step) {
-        const uint32_t t = step * TPS + slot;
-        if (t < nt) {
-            const uint4 x = step < kPre ? pre[step < kPre ? step : 0]
-                                        : *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
+        const uint32_t t = step * TPW + slot;
+        if (t < nw) {
+            const uint4 x = *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
             float v[VEC];
             if constexpr (VDT == kDtypeBF16) {
                 const uint32_t u[4] = {x.x, x.y, x.z, x.w};
@@ -2757,7 +2752,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const uint4* __restrict
             }
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-                const float wgt = e[j][t];
+                const float wgt = ew[j * 64 + t];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(wgt, v[k], o[j][k]);
             }
@@ -2773,13 +2768,34 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(const uint4* __restrict
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) red[wave][j][dc * VEC + k] = o[j][k];
+            for (int k = 0; k < VEC; ++k) ow[j * DV + dc * VEC + k] = o[j][k];
+    if (lane == 0)
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            wst[wave][j][0] = m[j];
+            wst[wave][j][1] = l[j];
+            wst[wave][j][2] = bad[j] ? 1.0f : 0.0f;
+        }
     __syncthreads();
+    // Merge the four waves: a wave with no token (m_w = -inf) weighs 0.
     for (uint32_t i = tid; i < group * DV; i += 256u) {
         const uint32_t j = i / DV, d = i % DV;
+        const float M = fmaxf(fmaxf(wst[0][j][0], wst[1][j][0]), fmaxf(wst[2][j][0], wst[3][j][0]));
+        float c[4], od[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            c[k] = wst[k][j][0] == -INFINITY ? 0.0f : __expf(wst[k][j][0] - M);
+            od[k] = reinterpret_cast<const float*>(tile_lds[k])[G * 64 + j * DV + d];
+        }
         float* pp = part + (((size_t)row * n_seg + seg) * group + j) * attn_partial_floats(DV);
-        pp[4 + d] = (red[0][j][d] + red[1][j][d]) + (red[2][j][d] + red[3][j][d]);
-        if (d == 0) pp[0] = m[j], pp[1] = nan[j] != 0.0f ? NAN : l[j];
+        pp[4 + d] = (od[0] * c[0] + od[1] * c[1]) + (od[2] * c[2] + od[3] * c[3]);
+        if (d == 0) {
+            const bool any_bad = (wst[0][j][2] + wst[1][j][2]) + (wst[2][j][2] + wst[3][j][2]) != 0.0f;
+            pp[0] = M;
+            pp[1] = any_bad ? NAN
+                            : (wst[0][j][1] * c[0] + wst[1][j][1] * c[1]) +
+                                  (wst[2][j][1] * c[2] + wst[3][j][1] * c[3]);
+        }
     }
 }
 
