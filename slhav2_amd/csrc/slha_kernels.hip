@@ -2504,6 +2504,7 @@ __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __rest
 // logits -inf) do not arise here.
 constexpr uint32_t kAttnSeg = 256;  // tokens per partial block (one per thread in phase 1)
 constexpr uint32_t kAttnMaxGroup = 16;
+constexpr uint32_t kAttnFusedMaxGroup = 4;  // groups scored inside attn_fused_kernel
 
 __host__ __device__ constexpr size_t attn_partial_floats(uint32_t d_v) { return (size_t)d_v + 4; }
 
@@ -2562,16 +2563,20 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     const char* vrow = static_cast<const char*>(vals) +
                        (((size_t)row * n_tok + t0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
     constexpr size_t kRowBytes = (size_t)DV * (VDT == kDtypeBF16 ? 2 : 4);
-    // The first kPre V vectors of this thread are loaded before the softmax
-    // reductions, so their latency overlaps the block's barriers.
-    constexpr uint32_t kSteps = kAttnSeg / TPS, kPre = kSteps < 8 ? kSteps : 8;
-    uint4 pre[kPre];
+    // V is read through a ring of kDepth 16-byte loads running ahead of the
+    // FMAs, at a token clamped into the segment (nt >= 1; no branch between
+    // the loads; a slot past the last token then uses V = 0). The ring is
+    // filled before the softmax reductions, so those loads overlap the
+    // block's barriers.
+    constexpr uint32_t kSteps = kAttnSeg / TPS, kDepth = kSteps < 8 ? kSteps : 8;
+    const auto load = [&](uint32_t step) {
+        const uint32_t t = step * TPS + slot;
+        const uint32_t tc = t < nt ? t : nt - 1u;
+        return *reinterpret_cast<const uint4*>(vrow + (size_t)tc * kRowBytes);
+    };
+    uint4 x[kDepth];
 #pragma unroll
-    for (uint32_t k = 0; k < kPre; ++k) {
-        const uint32_t t = k * TPS + slot;
-        pre[k] = t < nt ? *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes)
-                        : make_uint4(0u, 0u, 0u, 0u);
-    }
+    for (uint32_t u = 0; u < kDepth; ++u) x[u] = load(u);
     // phase 1
     float lg[G], m[G], l[G], nan[G];
 #pragma unroll
@@ -2602,28 +2607,29 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
 #pragma unroll
     for (uint32_t step = 0; step < kSteps; ++step) {
+        const uint4 cur = x[step % kDepth];
+        if (step + kDepth < kSteps) x[step % kDepth] = load(step + kDepth);
         const uint32_t t = step * TPS + slot;
-        if (t < nt) {
-            const uint4 x = step < kPre ? pre[step < kPre ? step : 0]
-                                        : *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
-            float v[VEC];
-            if constexpr (VDT == kDtypeBF16) {
-                const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+        const bool in = t < nt;
+        float v[VEC];
+        if constexpr (VDT == kDtypeBF16) {
+            const uint32_t u[4] = {cur.x, cur.y, cur.z, cur.w};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    v[2 * k] = __uint_as_float(u[k] << 16);
-                    v[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
-                }
-            } else {
-                v[0] = __uint_as_float(x.x), v[1] = __uint_as_float(x.y);
-                v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
+            for (int k = 0; k < 4; ++k) {
+                v[2 * k] = __uint_as_float(u[k] << 16);
+                v[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
             }
+        } else {
+            v[0] = __uint_as_float(cur.x), v[1] = __uint_as_float(cur.y);
+            v[2] = __uint_as_float(cur.z), v[3] = __uint_as_float(cur.w);
+        }
 #pragma unroll
-            for (int j = 0; j < G; ++j) {
-                const float w = e[j][t];
+        for (int k = 0; k < VEC; ++k) v[k] = in ? v[k] : 0.0f;
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(w, v[k], o[j][k]);
-            }
+        for (int j = 0; j < G; ++j) {
+            const float w = e[j][t < nt ? t : 0u];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(w, v[k], o[j][k]);
         }
     }
     // sum over the TPW token slots of the wave (lanes lane % LPT equal) ...
@@ -2648,7 +2654,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     }
 }
 
-// Fused segment kernel for group <= 4, grid (n_seg, n_rows), 256 threads.
+// Fused segment kernel for group <= kAttnFusedMaxGroup, grid (n_seg, n_rows), 256 threads.
 // Wave w scores tokens t0 + 64 w .. +63 exactly as score_rows_fast_kernel<4>
 // scores them (same tile DMA, query staging and MFMA paths) and runs a
 // flash-decoding step over its own 64 tokens: wave max m_w, weights
@@ -2665,7 +2671,7 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
                                                             const uint32_t* __restrict__ qs,
                                                             const void* __restrict__ vals,
                                                             float scale, float* __restrict__ part) {
-    constexpr int G = 4;
+    constexpr int G = (int)kAttnFusedMaxGroup;
     constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;  // V elements per 16-byte load
     constexpr int LPT = DV / VEC, TPW = 64 / LPT;   // lanes per token, tokens per wave step
     constexpr uint32_t kSteps = 64 / TPW;
@@ -2724,7 +2730,9 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
         l[j] = sm;
     }
     // o_w: lane group slot = lane / LPT reads token slot + TPW * step, dims
-    // dc * VEC .. +VEC-1, with one 16-byte load.
+    // dc * VEC .. +VEC-1, with one 16-byte load. Loads run 8 steps ahead in
+    // a ring, at a token clamped into the wave's range (no branch between
+    // them); a lane past the last token then uses V = 0.
     const uint32_t slot = lane / LPT, dc = lane % LPT;
     const char* vrow = static_cast<const char*>(vals) +
                        (((size_t)row * n_tok + wave0) * DV + (size_t)dc * VEC) * (VDT == kDtypeBF16 ? 2 : 4);
@@ -2733,26 +2741,39 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
     for (int j = 0; j < G; ++j)
 #pragma unroll
         for (int k = 0; k < VEC; ++k) o[j][k] = 0.0f;
+    if (nw > 0) {
+        constexpr uint32_t kDepth = kSteps < 8 ? kSteps : 8;
+        const auto load = [&](uint32_t step) {
+            const uint32_t t = step * TPW + slot;
+            const uint32_t tc = t < nw ? t : nw - 1u;
+            return *reinterpret_cast<const uint4*>(vrow + (size_t)tc * kRowBytes);
+        };
+        uint4 x[kDepth];
 #pragma unroll
-    for (uint32_t step = 0; step < kSteps; ++step) {
-        const uint32_t t = step * TPW + slot;
-        if (t < nw) {
-            const uint4 x = *reinterpret_cast<const uint4*>(vrow + (size_t)t * kRowBytes);
+        for (uint32_t u = 0; u < kDepth; ++u) x[u] = load(u);
+#pragma unroll
+        for (uint32_t step = 0; step < kSteps; ++step) {
+            const uint4 cur = x[step % kDepth];
+            if (step + kDepth < kSteps) x[step % kDepth] = load(step + kDepth);
+            const uint32_t t = step * TPW + slot;
+            const bool in = t < nw;
             float v[VEC];
             if constexpr (VDT == kDtypeBF16) {
-                const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+                const uint32_t w4[4] = {cur.x, cur.y, cur.z, cur.w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    v[2 * k] = __uint_as_float(u[k] << 16);
-                    v[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+                    v[2 * k] = __uint_as_float(w4[k] << 16);
+                    v[2 * k + 1] = __uint_as_float(w4[k] & 0xFFFF0000u);
                 }
             } else {
-                v[0] = __uint_as_float(x.x), v[1] = __uint_as_float(x.y);
-                v[2] = __uint_as_float(x.z), v[3] = __uint_as_float(x.w);
+                v[0] = __uint_as_float(cur.x), v[1] = __uint_as_float(cur.y);
+                v[2] = __uint_as_float(cur.z), v[3] = __uint_as_float(cur.w);
             }
 #pragma unroll
+            for (int k = 0; k < VEC; ++k) v[k] = in ? v[k] : 0.0f;
+#pragma unroll
             for (int j = 0; j < G; ++j) {
-                const float wgt = ew[j * 64 + t];
+                const float wgt = ew[j * 64 + (t & 63u)];
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) o[j][k] = fmaf(wgt, v[k], o[j][k]);
             }
@@ -2801,10 +2822,13 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
 
 // grid (n_rows * group, d_v / 16), 256 threads: thread (sl, c) = (tid / 16,
 // tid % 16) merges segments sl, sl + 16, ... for dim 16 blockIdx.y + c; the
-// 16 segment lanes are then added (xor shuffles, then LDS across waves).
+// 16 segment lanes are then added (xor shuffles, then LDS across waves). The
+// {m, l, o[d]} of a thread's first U segments are loaded together, before the
+// block max, so up to 16 U segments cost one round trip to memory.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
                                                            uint32_t n_seg, uint32_t group,
                                                            uint32_t d_v, float* __restrict__ out) {
+    constexpr uint32_t U = 8;
     __shared__ float red_a[4][16], red_l[4], red_m[4];
     __shared__ uint32_t red_n[4];
     const uint32_t qh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
@@ -2813,37 +2837,42 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     const uint32_t row = qh / group, j = qh % group;
     const size_t stride = (size_t)group * attn_partial_floats(d_v);  // one segment
     const float* p0 = part + ((size_t)row * n_seg * group + j) * attn_partial_floats(d_v);
+    // Segment s = sl + 16 u, read at min(s, n_seg - 1) and masked (n_seg >= 1).
+    float mu[U], lu[U], au[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t sg = sl + 16u * u;
+        const float* ps = p0 + (size_t)(sg < n_seg ? sg : n_seg - 1u) * stride;
+        mu[u] = ps[0], lu[u] = ps[1], au[u] = ps[4 + d];
+    }
     float M = -INFINITY;
-#pragma unroll 8
-    for (uint32_t s = sl; s < n_seg; s += 16u) M = fmaxf(M, p0[s * stride]);
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+        if (sl + 16u * u < n_seg) M = fmaxf(M, mu[u]);
+    for (uint32_t sg = sl + 16u * U; sg < n_seg; sg += 16u) M = fmaxf(M, p0[sg * stride]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
     if ((tid & 63u) == 0) red_m[wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-    // Eight segments per step with independent accumulators: their loads are
-    // in flight together.
-    constexpr uint32_t U = 8;
-    float Lu[U], Au[U];
-#pragma unroll
-    for (uint32_t u = 0; u < U; ++u) Lu[u] = 0.0f, Au[u] = 0.0f;
+    float L = 0.0f, acc = 0.0f;
     bool nan = false;
-    for (uint32_t s0 = sl; s0 < n_seg; s0 += 16u * U) {
 #pragma unroll
-        for (uint32_t u = 0; u < U; ++u) {
-            const uint32_t s = s0 + 16u * u;
-            if (s < n_seg) {
-                const float* ps = p0 + s * stride;
-                const float f = __expf(ps[0] - M);
-                nan = nan || isnan(ps[1]);
-                Lu[u] = fmaf(ps[1], f, Lu[u]);
-                Au[u] = fmaf(ps[4 + d], f, Au[u]);
-            }
+    for (uint32_t u = 0; u < U; ++u) {
+        if (sl + 16u * u < n_seg) {
+            const float f = __expf(mu[u] - M);
+            nan = nan || isnan(lu[u]);
+            L = fmaf(lu[u], f, L);
+            acc = fmaf(au[u], f, acc);
         }
     }
-    float L = 0.0f, acc = 0.0f;
-#pragma unroll
-    for (uint32_t u = 0; u < U; ++u) L += Lu[u], acc += Au[u];
+    for (uint32_t sg = sl + 16u * U; sg < n_seg; sg += 16u) {  // more than 16 U segments
+        const float* ps = p0 + sg * stride;
+        const float f = __expf(ps[0] - M);
+        nan = nan || isnan(ps[1]);
+        L = fmaf(ps[1], f, L);
+        acc = fmaf(ps[4 + d], f, acc);
+    }
     uint32_t nn = nan ? 1u : 0u;
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) {  // the 4 segment lanes of this wave
@@ -3129,9 +3158,7 @@ hipError_t attn_partial_dv(dim3 grid, const float* scores, const void* vals, uin
 template <int VDT>
 hipError_t attn_partial_g(dim3 grid, const float* scores, const void* vals, uint32_t n_tok,
                           uint32_t group, uint32_t d_v, float scale, float* part, hipStream_t s) {
-    if (group <= 1) return attn_partial_dv<VDT, 1>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
-    if (group <= 2) return attn_partial_dv<VDT, 2>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
-    if (group <= 4) return attn_partial_dv<VDT, 4>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
+    // group <= kAttnFusedMaxGroup runs attn_fused_kernel instead
     if (group <= 8) return attn_partial_dv<VDT, 8>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
     return attn_partial_dv<VDT, 16>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
 }
@@ -3147,10 +3174,11 @@ hipError_t attn_partial_dispatch(dim3 grid, const float* scores, const void* val
 size_t decode_attention_workspace_bytes(uint32_t n_rows, uint32_t n_tok, uint32_t group,
                                         uint32_t d_v) {
     const size_t n_seg = (n_tok + kAttnSeg - 1) / kAttnSeg;
-    const size_t scores = (size_t)n_rows * group * n_tok * 4;
     const size_t part = (size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4;
+    if (group <= kAttnFusedMaxGroup) return part;
+    const size_t scores = (size_t)n_rows * group * n_tok * 4;
     const size_t wide = score_rows_workspace_bytes(n_rows, group, false, false);
-    return ((scores + 255) & ~(size_t)255) + ((part + 255) & ~(size_t)255) + wide;
+    return ((part + 255) & ~(size_t)255) + ((scores + 255) & ~(size_t)255) + wide;
 }
 
 hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dtype,
@@ -3161,15 +3189,17 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
     if (group > kAttnMaxGroup || d_v < 32 || d_v > 256 || (d_v & (d_v - 1)) != 0)
         return hipErrorInvalidValue;
     const uint32_t n_seg = (n_tok + kAttnSeg - 1) / kAttnSeg;
+    // workspace: partials [n_rows][n_seg][group][d_v + 4], then (unfused
+    // groups only) scores [n_rows * group][n_tok] and the scorer's workspace
     char* ws = static_cast<char*>(workspace);
-    float* scores = reinterpret_cast<float*>(ws);
-    const size_t sb = ((size_t)n_rows * group * n_tok * 4 + 255) & ~(size_t)255;
-    float* part = reinterpret_cast<float*>(ws + sb);
+    float* part = reinterpret_cast<float*>(ws);
     const size_t pb = ((size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4 + 255) & ~(size_t)255;
+    float* scores = reinterpret_cast<float*>(ws + pb);
+    const size_t sb = ((size_t)n_rows * group * n_tok * 4 + 255) & ~(size_t)255;
     const uint4* tp = static_cast<const uint4*>(tiles);
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
     hipError_t e = hipSuccess;
-    if (group <= 4) {  // scores stay in LDS
+    if (group <= kAttnFusedMaxGroup) {  // scores stay in LDS
         const dim3 grid(n_seg, n_rows);
 #define SLHA_FUSED(VDT, DV)                                                                         \
     attn_fused_kernel<VDT, DV><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part)
