@@ -688,3 +688,57 @@ void orc_topk(const float* scores, size_t n, size_t k, uint32_t* idx_out, float*
     }
     free(all);
 }
+
+/* ------------------------------------------------------------------------ */
+/* EventLog records (eventlog.rs:82-100, 148-170, 330-352). */
+
+uint32_t orc_fnv1a(const uint8_t* p, size_t n) {
+    uint32_t h = 0x811C9DC5u;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 0x01000193u;
+    }
+    return h;
+}
+
+static void put_le(uint8_t* out, size_t* o, uint64_t v, int nbytes) {
+    for (int b = 0; b < nbytes; ++b) out[(*o)++] = (uint8_t)(v >> (8 * b));
+}
+
+void orc_tile_to_bytes(const orc_tile* t, uint8_t* out) {
+    size_t o = 0;
+    for (int i = 0; i < ORC_LATENT_BYTES; ++i) out[o++] = t->latent_kv[i];
+    for (int w = 0; w < ORC_RESIDUAL_WORDS; ++w) put_le(out, &o, t->residual_bitmap[w], 8);
+    uint32_t u;
+    memcpy(&u, &t->scale, 4);
+    put_le(out, &o, u, 4);
+    memcpy(&u, &t->dynamic_lambda, 4);
+    put_le(out, &o, u, 4);
+    memcpy(&u, &t->residual_sigma, 4);
+    put_le(out, &o, u, 4);
+    put_le(out, &o, t->token_id, 4);
+    put_le(out, &o, t->position, 4);
+    put_le(out, &o, t->head_id, 2);
+    put_le(out, &o, t->flags, 2);
+    for (int g = 0; g < ORC_N_GROUPS; ++g) out[o++] = t->group_scales[g];
+}
+
+uint32_t orc_record_checksum(uint64_t seq, uint32_t slot, const uint8_t* tile_bytes) {
+    uint8_t buf[8 + 4 + 128];
+    size_t o = 0;
+    put_le(buf, &o, seq, 8);
+    put_le(buf, &o, slot, 4);
+    memcpy(buf + o, tile_bytes, 128);
+    return orc_fnv1a(buf, sizeof buf);
+}
+
+void orc_eventlog_record(uint64_t seq, uint32_t slot, const orc_tile* t, uint32_t version,
+                         uint8_t* out) {
+    uint8_t tb[128];
+    orc_tile_to_bytes(t, tb);
+    size_t o = 0;
+    put_le(out, &o, seq, 8);
+    put_le(out, &o, slot, 4);
+    put_le(out, &o, version == 2 ? orc_record_checksum(seq, slot, tb) : 0u, 4);
+    memcpy(out + o, tb, 128);
+}

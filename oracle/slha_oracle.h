@@ -129,6 +129,16 @@ void orc_learned_decode(const float* p, const float* z, size_t d, size_t d_pad, 
 void orc_softmax_into(const float* scores, size_t n, float scale, float* out);
 void orc_aggregate_v(const float* weights, const float* values, size_t n, size_t d_v, float* out);
 
+/* eventlog.rs:82-100 — tile_to_bytes: the fields in the byte map's order,
+ * each little-endian. eventlog.rs:148-170 — FNV-1a 32 (offset 0x811C9DC5,
+ * prime 0x01000193) over seq (8 LE bytes) || slot (4) || tile bytes (128).
+ * orc_eventlog_record writes one 144-byte record (version 1: checksum 0). */
+uint32_t orc_fnv1a(const uint8_t* p, size_t n);
+void orc_tile_to_bytes(const orc_tile* t, uint8_t* out);
+uint32_t orc_record_checksum(uint64_t seq, uint32_t slot, const uint8_t* tile_bytes);
+void orc_eventlog_record(uint64_t seq, uint32_t slot, const orc_tile* t, uint32_t version,
+                         uint8_t* out);
+
 /* Batched helpers for tests (row-major inputs, one tile per key). */
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out);

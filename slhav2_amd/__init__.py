@@ -125,6 +125,18 @@ _SIGS = {
     "slha_gpu_decode_attention": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _P, _P, _SZ, ctypes.c_float,
                                          _P, _P]),
     "slha_gpu_synchronize": (_I32, [_P]),
+    "slha_eventlog_create": (_P, [ctypes.c_char_p, _I32]),
+    "slha_eventlog_open": (_P, [ctypes.c_char_p, _I32]),
+    "slha_eventlog_append": (_I32, [_P, _P, _SZ, _I32]),
+    "slha_eventlog_sync": (_I32, [_P]),
+    "slha_eventlog_len": (_U64, [_P]),
+    "slha_eventlog_version": (_U32, [_P]),
+    "slha_eventlog_read": (_I32, [_P, _U64, _SZ, _P]),
+    "slha_eventlog_find_seq": (_I32, [_P, _U64, _P, _P]),
+    "slha_eventlog_find_slot": (_I32, [_P, _U32, _P, _P]),
+    "slha_eventlog_close": (_I32, [_P]),
+    "slha_gpu_eventlog_pack": (_I32, [_P, _P, _P, _SZ, _U32, _P, _P]),
+    "slha_gpu_eventlog_unpack": (_I32, [_P, _SZ, _U32, _P, _P, _P, _P]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -481,3 +493,141 @@ def gpu_score_paged_topk(arena, page_tiles: int, page_table, max_pages: int, seq
 
 def synchronize(stream=None) -> None:
     _check(lib.slha_gpu_synchronize(_stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# EventLog (scirust/src/eventlog.rs) over the C ABI
+
+EVENTLOG_RECORD_BYTES = 144
+EVENTLOG_OPEN_STRICT, EVENTLOG_OPEN_RECOVER, EVENTLOG_OPEN_READ_ONLY = 0, 1, 2
+RECORD_DTYPE = None  # numpy structured dtype of one record, set on first use
+
+
+def record_dtype():
+    """numpy dtype of one 144-byte record: seq u64, slot u32, checksum u32, tile 128 B."""
+    global RECORD_DTYPE
+    if RECORD_DTYPE is None:
+        import numpy as np
+
+        RECORD_DTYPE = np.dtype([("seq", "<u8"), ("slot", "<u4"), ("checksum", "<u4"), ("tile", "u1", 128)])
+    return RECORD_DTYPE
+
+
+class EventLog:
+    """Mirror of `EventLog` (eventlog.rs:179-486): create / create_new / open /
+    open_recover / open_read_only, append / append_durable of packed records,
+    len, sync, read_all, fetch_by_seq, fetch_last_for_slot. Errors raise
+    SlhaError with the reference's messages ("EventLog: bad magic", ...)."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @classmethod
+    def _made(cls, h):
+        if not h:
+            raise SlhaError(ERR_IO, last_error())
+        return cls(h)
+
+    @classmethod
+    def create(cls, path) -> "EventLog":
+        return cls._made(lib.slha_eventlog_create(os.fsencode(path), 0))
+
+    @classmethod
+    def create_new(cls, path) -> "EventLog":
+        return cls._made(lib.slha_eventlog_create(os.fsencode(path), 1))
+
+    @classmethod
+    def open(cls, path, mode: int = EVENTLOG_OPEN_STRICT) -> "EventLog":
+        return cls._made(lib.slha_eventlog_open(os.fsencode(path), mode))
+
+    @classmethod
+    def open_recover(cls, path) -> "EventLog":
+        return cls.open(path, EVENTLOG_OPEN_RECOVER)
+
+    @classmethod
+    def open_read_only(cls, path) -> "EventLog":
+        return cls.open(path, EVENTLOG_OPEN_READ_ONLY)
+
+    def append(self, records, durable: bool = False) -> None:
+        """records: numpy array of record_dtype() (or raw bytes, 144 per record)."""
+        import numpy as np
+
+        buf = np.ascontiguousarray(np.frombuffer(memoryview(records).cast("B"), dtype=np.uint8))
+        if buf.size % EVENTLOG_RECORD_BYTES:
+            raise ValueError("records must be a whole number of 144-byte records")
+        _check(lib.slha_eventlog_append(self._h, buf.ctypes.data, buf.size // EVENTLOG_RECORD_BYTES,
+                                        1 if durable else 0))
+
+    def append_durable(self, records) -> None:
+        self.append(records, durable=True)
+
+    def __len__(self) -> int:
+        n = lib.slha_eventlog_len(self._h)
+        if n == 0 and last_error():
+            raise SlhaError(ERR_INVALID_HANDLE, last_error())
+        return n
+
+    @property
+    def version(self) -> int:
+        return lib.slha_eventlog_version(self._h)
+
+    def sync(self) -> None:
+        _check(lib.slha_eventlog_sync(self._h))
+
+    def read(self, first: int = 0, n: int | None = None):
+        import numpy as np
+
+        if n is None:
+            n = len(self) - first
+        out = np.zeros(n, dtype=record_dtype())
+        _check(lib.slha_eventlog_read(self._h, first, n, out.ctypes.data if n else None))
+        return out
+
+    def read_all(self):
+        return self.read(0)
+
+    def _find(self, fn, key):
+        idx, found = ctypes.c_uint64(0), ctypes.c_int32(0)
+        _check(fn(self._h, key, ctypes.byref(idx), ctypes.byref(found)))
+        return self.read(idx.value, 1)[0] if found.value else None
+
+    def fetch_by_seq(self, seq: int):
+        return self._find(lib.slha_eventlog_find_seq, seq)
+
+    def fetch_last_for_slot(self, slot: int):
+        return self._find(lib.slha_eventlog_find_slot, slot)
+
+    def close(self) -> None:
+        if self._h:
+            _check(lib.slha_eventlog_close(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def gpu_eventlog_pack(arena, slots, seqs, version: int = 2, stream=None):
+    """Records (uint8 GPU tensor [n, 144]) of arena tiles `slots` (int32 [n])
+    with insertion sequence numbers `seqs` (int64 [n]) - ElasticKvCache::evict."""
+    import torch
+
+    n = slots.numel()
+    rec = torch.empty((n, EVENTLOG_RECORD_BYTES), dtype=torch.uint8, device=arena.device)
+    _check(lib.slha_gpu_eventlog_pack(_dev_ptr(arena.reshape(-1, 128)), _dev_ptr(slots), _dev_ptr(seqs), n,
+                                      version, _dev_ptr(rec), _stream(stream)))
+    return rec
+
+
+def gpu_eventlog_unpack(records, dst_slots, arena, version: int = 2, stream=None):
+    """Writes each record's tile into arena slot dst_slots[i] when its checksum
+    holds; returns the int32 status [n] (0 restored, 1 checksum mismatch)."""
+    import torch
+
+    n = dst_slots.numel()
+    status = torch.empty(n, dtype=torch.int32, device=arena.device)
+    _check(lib.slha_gpu_eventlog_unpack(_dev_ptr(records), n, version, _dev_ptr(dst_slots),
+                                        _dev_ptr(arena.reshape(-1, 128)), _dev_ptr(status), _stream(stream)))
+    return status

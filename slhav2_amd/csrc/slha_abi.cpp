@@ -11,7 +11,9 @@
 // through per-thread device memory on a per-thread stream.
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
 #include <sys/stat.h>
+#include <unistd.h>
 
 #include <cerrno>
 #include <cmath>
@@ -27,6 +29,7 @@
 #include <vector>
 
 #include "../../include/slha.h"
+#include "../../include/slha_eventlog.h"
 #include "../../include/slha_gpu.h"
 #include "slha_launch.h"
 
@@ -1094,6 +1097,321 @@ int32_t slha_gpu_synchronize(void* stream) {
         require_device();
         check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
         check_hip(hipGetLastError(), "pending HIP error");
+    });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// EventLog (scirust/src/eventlog.rs): the file side on POSIX descriptors.
+
+namespace {
+
+constexpr uint32_t kLogMagic = SLHA_EVENTLOG_MAGIC;
+constexpr uint32_t kLogV1 = 1, kLogV2 = 2;
+constexpr size_t kLogHeader = SLHA_EVENTLOG_HEADER_BYTES, kLogRecord = SLHA_EVENTLOG_RECORD_BYTES;
+constexpr size_t kLogChunk = 4096;  // records per read while validating
+
+struct EventLogObj {
+    int fd = -1;
+    uint64_t records = 0;
+    uint32_t version = kLogV2;
+    bool writable = true;
+    std::mutex mu;
+    ~EventLogObj() {
+        if (fd >= 0) ::close(fd);
+    }
+};
+
+struct LogRegistry {
+    std::mutex mu;
+    std::unordered_map<uintptr_t, std::unique_ptr<EventLogObj>> live;
+};
+
+LogRegistry& log_registry() {
+    static LogRegistry* r = new LogRegistry();
+    return *r;
+}
+
+// Handles are small never-freed tokens, so a closed handle cannot alias a
+// later one.
+SlhaEventLog* register_log(std::unique_ptr<EventLogObj> obj) {
+    SlhaEventLog* token = reinterpret_cast<SlhaEventLog*>(new uint64_t(0));
+    auto& r = log_registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    r.live.emplace(reinterpret_cast<uintptr_t>(token), std::move(obj));
+    return token;
+}
+
+EventLogObj* log_of(const SlhaEventLog* log) {
+    if (!log) fail(SLHA_ERR_NULL, "EventLog handle is NULL");
+    auto& r = log_registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    auto it = r.live.find(reinterpret_cast<uintptr_t>(log));
+    if (it == r.live.end()) fail(SLHA_ERR_INVALID_HANDLE, "EventLog handle is not a live SLHA handle");
+    return it->second.get();
+}
+
+[[noreturn]] void io_fail(const char* what) {
+    fail(SLHA_ERR_IO, "EventLog: %s: %s", what, std::strerror(errno));
+}
+
+void write_all(int fd, const uint8_t* p, size_t n, uint64_t off) {
+    while (n > 0) {
+        const ssize_t w = ::pwrite(fd, p, n, (off_t)off);
+        if (w < 0) {
+            if (errno == EINTR) continue;
+            io_fail("write");
+        }
+        p += w, n -= (size_t)w, off += (uint64_t)w;
+    }
+}
+
+void read_all(int fd, uint8_t* p, size_t n, uint64_t off) {
+    while (n > 0) {
+        const ssize_t r = ::pread(fd, p, n, (off_t)off);
+        if (r < 0) {
+            if (errno == EINTR) continue;
+            io_fail("read");
+        }
+        if (r == 0) fail(SLHA_ERR_IO, "EventLog: unexpected end of file");
+        p += r, n -= (size_t)r, off += (uint64_t)r;
+    }
+}
+
+uint64_t le64(const uint8_t* p) { return (uint64_t)le32(p) | (uint64_t)le32(p + 4) << 32; }
+
+// eventlog.rs:148-170: FNV-1a 32 over the record's seq and slot (bytes 0..12)
+// and its tile (bytes 16..144).
+uint32_t record_checksum(const uint8_t* rec) {
+    uint32_t h = 0x811C9DC5u;
+    for (size_t i = 0; i < 12; ++i) h = (h ^ rec[i]) * 0x01000193u;
+    for (size_t i = 16; i < kLogRecord; ++i) h = (h ^ rec[i]) * 0x01000193u;
+    return h;
+}
+
+// decode_record (eventlog.rs:412-435): version 2 checks the stored checksum.
+bool record_ok(const uint8_t* rec, uint32_t version) {
+    return version != kLogV2 || le32(rec + 12) == record_checksum(rec);
+}
+
+// Visits every record in order, in chunks, failing on a bad checksum.
+template <class F>
+void scan_records(EventLogObj* L, F&& visit) {
+    std::vector<uint8_t> buf(kLogChunk * kLogRecord);
+    for (uint64_t i0 = 0; i0 < L->records; i0 += kLogChunk) {
+        const size_t m = (size_t)std::min<uint64_t>(kLogChunk, L->records - i0);
+        read_all(L->fd, buf.data(), m * kLogRecord, kLogHeader + i0 * kLogRecord);
+        for (size_t i = 0; i < m; ++i) {
+            const uint8_t* rec = buf.data() + i * kLogRecord;
+            if (!record_ok(rec, L->version)) fail(SLHA_ERR_IO, "EventLog: record checksum mismatch");
+            visit(i0 + i, rec);
+        }
+    }
+}
+
+void check_path(const char* path) {
+    if (!path) fail(SLHA_ERR_NULL, "EventLog path is NULL");
+}
+
+}  // namespace
+
+extern "C" {
+
+SlhaEventLog* slha_eventlog_create(const char* path, int32_t exclusive) {
+    SlhaEventLog* out = nullptr;
+    const int32_t rc = ffi_status([&] {
+        check_path(path);
+        auto L = std::make_unique<EventLogObj>();
+        L->fd = ::open(path, O_RDWR | O_CREAT | O_CLOEXEC | (exclusive ? O_EXCL : O_TRUNC), 0644);
+        if (L->fd < 0) io_fail(exclusive && errno == EEXIST ? "refusing to overwrite an existing log" : "create");
+        uint8_t h[kLogHeader] = {0};
+        const uint32_t fields[3] = {kLogMagic, kLogV2, 128u};
+        for (int k = 0; k < 3; ++k)
+            for (int b = 0; b < 4; ++b) h[4 * k + b] = (uint8_t)(fields[k] >> (8 * b));
+        write_all(L->fd, h, sizeof h, 0);
+        out = register_log(std::move(L));
+    });
+    return rc == SLHA_OK ? out : nullptr;
+}
+
+SlhaEventLog* slha_eventlog_open(const char* path, int32_t mode) {
+    SlhaEventLog* out = nullptr;
+    const int32_t rc = ffi_status([&] {
+        check_path(path);
+        if (mode < SLHA_EVENTLOG_OPEN_STRICT || mode > SLHA_EVENTLOG_OPEN_READ_ONLY)
+            fail(SLHA_ERR_DIMENSION, "unknown EventLog open mode %d", mode);
+        auto L = std::make_unique<EventLogObj>();
+        L->writable = mode != SLHA_EVENTLOG_OPEN_READ_ONLY;
+        L->fd = ::open(path, (L->writable ? O_RDWR : O_RDONLY) | O_CLOEXEC);
+        if (L->fd < 0) io_fail("open");
+        struct stat st;
+        if (::fstat(L->fd, &st) != 0) io_fail("stat");
+        uint64_t len = (uint64_t)st.st_size;
+        if (len < kLogHeader) fail(SLHA_ERR_IO, "EventLog: file shorter than header");
+        uint8_t h[kLogHeader];
+        read_all(L->fd, h, sizeof h, 0);
+        if (le32(h) != kLogMagic) fail(SLHA_ERR_IO, "EventLog: bad magic");
+        L->version = le32(h + 4);
+        if (L->version != kLogV1 && L->version != kLogV2) fail(SLHA_ERR_IO, "EventLog: unsupported version");
+        if (le32(h + 8) != 128u) fail(SLHA_ERR_IO, "EventLog: tile-size mismatch");
+        const uint64_t rem = (len - kLogHeader) % kLogRecord;
+        if (rem != 0) {
+            if (mode != SLHA_EVENTLOG_OPEN_RECOVER) fail(SLHA_ERR_IO, "EventLog: truncated record");
+            len -= rem;
+            if (::ftruncate(L->fd, (off_t)len) != 0) io_fail("truncate");
+            if (::fsync(L->fd) != 0) io_fail("sync");
+        }
+        L->records = (len - kLogHeader) / kLogRecord;
+        scan_records(L.get(), [](uint64_t, const uint8_t*) {});
+        out = register_log(std::move(L));
+    });
+    return rc == SLHA_OK ? out : nullptr;
+}
+
+int32_t slha_eventlog_append(SlhaEventLog* log, const uint8_t* records, size_t n, int32_t durable) {
+    return ffi_status([&] {
+        EventLogObj* L = log_of(log);
+        std::lock_guard<std::mutex> lock(L->mu);
+        if (!L->writable) fail(SLHA_ERR_IO, "EventLog: log opened read-only");
+        if (n == 0) return;
+        if (!records) fail(SLHA_ERR_NULL, "slha_eventlog_append received a NULL pointer");
+        for (size_t i = 0; i < n; ++i) {
+            const uint8_t* rec = records + i * kLogRecord;
+            const uint32_t want = L->version == kLogV2 ? record_checksum(rec) : 0u;
+            if (le32(rec + 12) != want)
+                fail(SLHA_ERR_INVALID_TILE, "EventLog: record %zu checksum is not the version-%u value", i,
+                     L->version);
+        }
+        const uint64_t start = kLogHeader + L->records * kLogRecord;
+        try {
+            write_all(L->fd, records, n * kLogRecord, start);
+            if (durable && ::fsync(L->fd) != 0) io_fail("sync");
+        } catch (...) {
+            if (::ftruncate(L->fd, (off_t)start) == 0 && durable) (void)::fsync(L->fd);
+            throw;
+        }
+        L->records += n;
+    });
+}
+
+int32_t slha_eventlog_sync(SlhaEventLog* log) {
+    return ffi_status([&] {
+        EventLogObj* L = log_of(log);
+        std::lock_guard<std::mutex> lock(L->mu);
+        if (L->writable && ::fsync(L->fd) != 0) io_fail("sync");
+    });
+}
+
+uint64_t slha_eventlog_len(const SlhaEventLog* log) {
+    uint64_t n = 0;
+    const int32_t rc = ffi_status([&] {
+        EventLogObj* L = log_of(log);
+        std::lock_guard<std::mutex> lock(L->mu);
+        n = L->records;
+    });
+    return rc == SLHA_OK ? n : 0;
+}
+
+uint32_t slha_eventlog_version(const SlhaEventLog* log) {
+    uint32_t v = 0;
+    const int32_t rc = ffi_status([&] { v = log_of(log)->version; });
+    return rc == SLHA_OK ? v : 0;
+}
+
+int32_t slha_eventlog_read(SlhaEventLog* log, uint64_t first, size_t n, uint8_t* records_out) {
+    return ffi_status([&] {
+        EventLogObj* L = log_of(log);
+        std::lock_guard<std::mutex> lock(L->mu);
+        if (first > L->records || n > L->records - first)
+            fail(SLHA_ERR_DIMENSION, "EventLog: records [%llu, %llu) out of range (len %llu)",
+                 (unsigned long long)first, (unsigned long long)(first + n),
+                 (unsigned long long)L->records);
+        if (n == 0) return;
+        if (!records_out) fail(SLHA_ERR_NULL, "slha_eventlog_read received a NULL pointer");
+        read_all(L->fd, records_out, n * kLogRecord, kLogHeader + first * kLogRecord);
+        for (size_t i = 0; i < n; ++i)
+            if (!record_ok(records_out + i * kLogRecord, L->version))
+                fail(SLHA_ERR_IO, "EventLog: record checksum mismatch");
+    });
+}
+
+static int32_t find_latest(SlhaEventLog* log, uint64_t* index_out, int32_t* found,
+                           bool (*match)(const uint8_t*, uint64_t), uint64_t key) {
+    return ffi_status([&] {
+        if (!index_out || !found) fail(SLHA_ERR_NULL, "EventLog lookup received a NULL pointer");
+        EventLogObj* L = log_of(log);
+        std::lock_guard<std::mutex> lock(L->mu);
+        bool hit = false;
+        uint64_t at = 0;
+        scan_records(L, [&](uint64_t i, const uint8_t* rec) {
+            if (match(rec, key)) hit = true, at = i;
+        });
+        *found = hit ? 1 : 0;
+        *index_out = at;
+    });
+}
+
+int32_t slha_eventlog_find_seq(SlhaEventLog* log, uint64_t seq, uint64_t* index_out, int32_t* found) {
+    return find_latest(log, index_out, found, [](const uint8_t* r, uint64_t k) { return le64(r) == k; }, seq);
+}
+
+int32_t slha_eventlog_find_slot(SlhaEventLog* log, uint32_t slot, uint64_t* index_out, int32_t* found) {
+    return find_latest(log, index_out, found, [](const uint8_t* r, uint64_t k) { return le32(r + 8) == k; },
+                       slot);
+}
+
+int32_t slha_eventlog_close(SlhaEventLog* log) {
+    return ffi_status([&] {
+        if (!log) fail(SLHA_ERR_NULL, "EventLog handle is NULL");
+        std::unique_ptr<EventLogObj> obj;
+        {
+            auto& r = log_registry();
+            std::lock_guard<std::mutex> lock(r.mu);
+            auto it = r.live.find(reinterpret_cast<uintptr_t>(log));
+            if (it == r.live.end()) fail(SLHA_ERR_INVALID_HANDLE, "EventLog handle is not a live SLHA handle");
+            obj = std::move(it->second);
+            r.live.erase(it);
+        }
+        std::lock_guard<std::mutex> lock(obj->mu);  // waits for a call in flight
+    });
+}
+
+int32_t slha_gpu_eventlog_pack(const SciRustSlhaTile* arena_dev, const uint32_t* slots_dev,
+                               const uint64_t* seqs_dev, size_t n, uint32_t version,
+                               uint8_t* records_dev, void* stream) {
+    return ffi_status([&] {
+        if (version != kLogV1 && version != kLogV2)
+            fail(SLHA_ERR_DIMENSION, "EventLog version %u is not 1 or 2", version);
+        if (n > ((uint64_t)INT32_MAX) * 256u) fail(SLHA_ERR_DIMENSION, "n=%zu records out of range", n);
+        if (n == 0) return;
+        if (!arena_dev || !slots_dev || !seqs_dev || !records_dev)
+            fail(SLHA_ERR_NULL, "slha_gpu_eventlog_pack received a NULL pointer");
+        if (reinterpret_cast<uintptr_t>(records_dev) % 16 != 0)
+            fail(SLHA_ERR_DIMENSION, "records_dev must be 16-byte aligned");
+        require_device();
+        check_hip(launch_eventlog_pack(arena_dev, slots_dev, seqs_dev, n, version, records_dev,
+                                       static_cast<hipStream_t>(stream)),
+                  "eventlog pack kernel");
+    });
+}
+
+int32_t slha_gpu_eventlog_unpack(const uint8_t* records_dev, size_t n, uint32_t version,
+                                 const uint32_t* dst_slots_dev, SciRustSlhaTile* arena_dev,
+                                 uint32_t* status_dev, void* stream) {
+    return ffi_status([&] {
+        if (version != kLogV1 && version != kLogV2)
+            fail(SLHA_ERR_DIMENSION, "EventLog version %u is not 1 or 2", version);
+        if (n > ((uint64_t)INT32_MAX) * 256u) fail(SLHA_ERR_DIMENSION, "n=%zu records out of range", n);
+        if (n == 0) return;
+        if (!records_dev || !dst_slots_dev || !arena_dev || !status_dev)
+            fail(SLHA_ERR_NULL, "slha_gpu_eventlog_unpack received a NULL pointer");
+        if (reinterpret_cast<uintptr_t>(records_dev) % 16 != 0)
+            fail(SLHA_ERR_DIMENSION, "records_dev must be 16-byte aligned");
+        require_device();
+        check_hip(launch_eventlog_unpack(records_dev, n, version, dst_slots_dev, arena_dev, status_dev,
+                                         static_cast<hipStream_t>(stream)),
+                  "eventlog unpack kernel");
     });
 }
 

@@ -11,6 +11,9 @@
 //   decode_kernel          tile -> latent (+ sign-sketch residual) (learned.rs:283-321)
 //   validate_kernel        slha-c/src/lib.rs:244-286 on device
 //   ccos_apply_kernel      page_out / drop_correction (ccos.rs:369-397)
+//   learned_*_kernel       d > 128 LearnedModel encode / query / decode (learned.rs:257-408)
+//   attn_*_kernel          decode attention softmax(s * scale) . V (benchmark_decode.rs:29-90)
+//   eventlog_*_kernel      EventLog records of evicted tiles, and rehydrate (eventlog.rs:9-36)
 #include "slha_device.h"
 #include "slha_launch.h"
 
@@ -2892,6 +2895,102 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------------------
+// EventLog records (eventlog.rs:9-36): 144 bytes = u64 seq, u32 slot, u32
+// checksum, the 128 tile bytes. The tile's in-memory bytes are already the
+// little-endian serialisation of `tile_to_bytes` (eventlog.rs:82-100), so a
+// record is the tile copied behind a 16-byte head. Version 2's checksum is
+// FNV-1a 32 over seq || slot || tile (eventlog.rs:148-170); version 1 stores 0.
+
+constexpr uint32_t kFnvOffset = 0x811C9DC5u, kFnvPrime = 0x01000193u;
+
+__device__ __forceinline__ uint32_t fnv_word(uint32_t h, uint32_t w) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) h = (h ^ ((w >> (8 * b)) & 0xFFu)) * kFnvPrime;
+    return h;
+}
+
+__device__ __forceinline__ uint32_t record_checksum(uint64_t seq, uint32_t slot, const uint4* t) {
+    uint32_t h = fnv_word(kFnvOffset, (uint32_t)seq);
+    h = fnv_word(h, (uint32_t)(seq >> 32));
+    h = fnv_word(h, slot);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        h = fnv_word(h, t[j].x);
+        h = fnv_word(h, t[j].y);
+        h = fnv_word(h, t[j].z);
+        h = fnv_word(h, t[j].w);
+    }
+    return h;
+}
+
+constexpr uint32_t kRecordQuads = 9;  // 144 B
+
+// 256 records per workgroup: thread r gathers tile slots[r] (8 x 16-byte
+// loads), hashes it and writes its record into LDS; the workgroup then stores
+// its 36 KiB of records with consecutive 16-byte stores.
+__global__ __launch_bounds__(256) void eventlog_pack_kernel(const uint4* __restrict__ arena,
+                                                            const uint32_t* __restrict__ slots,
+                                                            const uint64_t* __restrict__ seqs,
+                                                            uint64_t n, uint32_t version,
+                                                            uint4* __restrict__ records) {
+    __shared__ uint4 rec[256 * kRecordQuads];
+    const uint64_t base = (uint64_t)blockIdx.x * 256u;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t cnt = n - base < 256u ? (uint32_t)(n - base) : 256u;
+    if (tid < cnt) {
+        const uint64_t seq = seqs[base + tid];
+        const uint32_t slot = slots[base + tid];
+        uint4 t[8];
+        const uint4* src = arena + (size_t)slot * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = src[j];
+        const uint32_t ck = version >= 2 ? record_checksum(seq, slot, t) : 0u;
+        uint4* r = rec + tid * kRecordQuads;
+        r[0] = make_uint4((uint32_t)seq, (uint32_t)(seq >> 32), slot, ck);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[1 + j] = t[j];
+    }
+    __syncthreads();
+    uint4* out = records + base * kRecordQuads;
+    for (uint32_t q = tid; q < cnt * kRecordQuads; q += 256u) out[q] = rec[q];
+}
+
+// The reverse: 256 records per workgroup are loaded with consecutive 16-byte
+// loads into LDS; thread r checks record r's checksum (version 2) and, when it
+// holds, writes the tile into slot dst[r] and status 0; otherwise the slot is
+// left untouched and status is 1.
+__global__ __launch_bounds__(256) void eventlog_unpack_kernel(const uint4* __restrict__ records,
+                                                              uint64_t n, uint32_t version,
+                                                              const uint32_t* __restrict__ dst,
+                                                              uint4* __restrict__ arena,
+                                                              uint32_t* __restrict__ status) {
+    __shared__ uint4 rec[256 * kRecordQuads];
+    const uint64_t base = (uint64_t)blockIdx.x * 256u;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t cnt = n - base < 256u ? (uint32_t)(n - base) : 256u;
+    const uint4* in = records + base * kRecordQuads;
+    for (uint32_t q = tid; q < cnt * kRecordQuads; q += 256u) rec[q] = in[q];
+    __syncthreads();
+    if (tid >= cnt) return;
+    const uint4* r = rec + tid * kRecordQuads;
+    const uint4 head = r[0];
+    uint4 t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = r[1 + j];
+    bool ok = true;
+    if (version >= 2) {
+        const uint64_t seq = (uint64_t)head.x | ((uint64_t)head.y << 32);
+        ok = record_checksum(seq, head.z, t) == head.w;
+    }
+    if (ok) {
+        uint4* d = arena + (size_t)dst[base + tid] * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d[j] = t[j];
+    }
+    status[base + tid] = ok ? 0u : 1u;
+}
+
+// ---------------------------------------------------------------------------
 // Launchers
 
 size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
@@ -3255,6 +3354,22 @@ __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t value) {
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t value, hipStream_t s) {
     if (n == 0) return hipSuccess;
     fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_eventlog_pack(const void* arena, const uint32_t* slots, const uint64_t* seqs,
+                                uint64_t n, uint32_t version, void* records, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    eventlog_pack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        static_cast<const uint4*>(arena), slots, seqs, n, version, static_cast<uint4*>(records));
+    return hipGetLastError();
+}
+
+hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t version,
+                                  const uint32_t* dst, void* arena, uint32_t* status, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    eventlog_unpack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        static_cast<const uint4*>(records), n, version, dst, static_cast<uint4*>(arena), status);
     return hipGetLastError();
 }
 

@@ -93,6 +93,11 @@ hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, 
                          float* out, hipStream_t s);
 hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s);
 hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s);
+// EventLog records (144 B each, eventlog.rs:9-36); n < 2^31 * 256.
+hipError_t launch_eventlog_pack(const void* arena, const uint32_t* slots, const uint64_t* seqs,
+                                uint64_t n, uint32_t version, void* records, hipStream_t s);
+hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t version,
+                                  const uint32_t* dst, void* arena, uint32_t* status, hipStream_t s);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t value, hipStream_t s);
 

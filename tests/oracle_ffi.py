@@ -88,6 +88,10 @@ for name, res, args in [
     ("orc_learned_decode", None, [_P, _P, _SZ, _SZ, ctypes.c_int, _P, ctypes.c_int, _P]),
     ("orc_softmax_into", None, [_P, _SZ, _F, _P]),
     ("orc_aggregate_v", None, [_P, _P, _SZ, _SZ, _P]),
+    ("orc_fnv1a", ctypes.c_uint32, [_P, _SZ]),
+    ("orc_tile_to_bytes", None, [_P, _P]),
+    ("orc_record_checksum", ctypes.c_uint32, [ctypes.c_uint64, ctypes.c_uint32, _P]),
+    ("orc_eventlog_record", None, [ctypes.c_uint64, ctypes.c_uint32, _P, ctypes.c_uint32, _P]),
 ]:
     fn = getattr(lib, name)
     fn.restype = res
@@ -338,3 +342,30 @@ def decode_attention(tiles, values, q_coarse, q_sign, scale: float) -> np.ndarra
     softmax_into, aggregate_v (benchmark_decode.rs:84-90)."""
     sc, _ = score(tiles, q_coarse, q_sign)
     return aggregate(softmax(sc, scale), values)
+
+
+# --------------------------------------------------------------------------
+# EventLog records (eventlog.rs:82-100, 148-170)
+
+def fnv1a(data: bytes) -> int:
+    b = np.frombuffer(bytes(data), np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    return int(lib.orc_fnv1a(_p(b), len(data)))
+
+
+def tile_to_bytes(tile) -> bytes:
+    t = np.ascontiguousarray(tile, TILE_DTYPE).reshape(-1)
+    out = np.zeros(128, np.uint8)
+    lib.orc_tile_to_bytes(_p(t), _p(out))
+    return out.tobytes()
+
+
+def eventlog_records(tiles, slots, seqs, version: int = 2) -> np.ndarray:
+    """144-byte records of tiles[slots[i]] with seq seqs[i] (uint8 [n, 144])."""
+    t = np.ascontiguousarray(tiles, TILE_DTYPE).reshape(-1)
+    out = np.zeros((len(slots), 144), np.uint8)
+    for i, (sl, sq) in enumerate(zip(slots, seqs)):
+        one = np.ascontiguousarray(t[int(sl)]).reshape(1)
+        row = np.zeros(144, np.uint8)
+        lib.orc_eventlog_record(int(sq), int(sl), _p(one), version, _p(row))
+        out[i] = row
+    return out
