@@ -448,6 +448,52 @@ def run_c5(args) -> int:
     return 0
 
 
+def run_evict(args) -> int:
+    """EventLog eviction and rehydrate on the GPU (ccos.rs:404-466,
+    eventlog.rs:330-352): one step packs the records of 1 M random slots of a
+    4 M-tile arena (512 MiB) - seq, slot, FNV-1a checksum and the tile - and a
+    second timed loop unpacks 1 M records into random slots with their
+    checksums checked. Per record: pack reads 4 + 8 + 128 B and writes 144 B;
+    unpack reads 144 + 4 B and writes 128 + 4 B."""
+    import torch
+
+    import slhav2_amd as s
+
+    n_arena, n = 1 << 22, 1 << 20
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(0x5EED000A)
+    arena = torch.randint(0, 256, (n_arena, 128), dtype=torch.uint8, device="cuda", generator=g)
+    sets = []
+    for _ in range(2):
+        slots = torch.randperm(n_arena, device="cuda", generator=g)[:n].to(torch.int32)
+        seqs = torch.randint(0, 1 << 62, (n,), dtype=torch.int64, device="cuda", generator=g)
+        rec = torch.empty((n, 144), dtype=torch.uint8, device="cuda")
+        dst = torch.randperm(n_arena, device="cuda", generator=g)[:n].to(torch.int32)
+        status = torch.empty(n, dtype=torch.int32, device="cuda")
+        sets.append((slots, seqs, rec, dst, status))
+    vp = ctypes.c_void_p
+    pack_args = [(vp(arena.data_ptr()), vp(sl.data_ptr()), vp(sq.data_ptr()), n, 2, vp(r.data_ptr()),
+                  vp(stream.cuda_stream)) for sl, sq, r, _, _ in sets]
+    unpack_args = [(vp(r.data_ptr()), n, 2, vp(d.data_ptr()), vp(arena.data_ptr()), vp(st.data_ptr()),
+                    vp(stream.cuda_stream)) for _, _, r, d, st in sets]
+    pack, unpack = s.lib.slha_gpu_eventlog_pack, s.lib.slha_gpu_eventlog_unpack
+    steps, warmup = min(args.steps, 100), min(args.warmup, 10)
+    ms_pack = timed_steps(lambda i: pack(*pack_args[i % 2]), steps, warmup, stream)
+    ms_unpack = timed_steps(lambda i: unpack(*unpack_args[i % 2]), steps, warmup, stream)
+    assert int(sets[0][4].sum().item()) == 0, "records failed their checksum"
+    b_pack, b_unpack = n * (4 + 8 + 128 + 144), n * (144 + 4 + 128 + 4)
+    print(json.dumps(line(
+        "EventLog records packed/s (evict: gather + FNV-1a, 1 M of a 4 M-tile arena)", n / (ms_pack * 1e-3),
+        "records/s", steps, warmup, ms_pack, "u8",
+        {"workload": "EventLog evict/rehydrate (eventlog.rs records on the GPU)", "arena_tiles": n_arena,
+         "records_per_step": n, "version": 2, "parallelism": "none (1 GPU)"},
+        roofline=hbm_roofline(b_pack, ms_pack, "slha::eventlog_pack_kernel", "evict"),
+        unpack={"records_per_s": n / (ms_unpack * 1e-3), "ms_per_launch": ms_unpack,
+                "roofline": hbm_roofline(b_unpack, ms_unpack, "slha::eventlog_unpack_kernel", "rehydrate")})),
+        flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -456,7 +502,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict"], default="c2",
                     help="c2 (default) is the headline; c3/c4/c5 measure the other "
                          "BASELINE configs at full size")
     args = ap.parse_args()
@@ -469,7 +515,8 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration()
     if args.config != "c2":
-        return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode}[args.config](args)
+        return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode,
+                "evict": run_evict}[args.config](args)
 
     import torch
 
