@@ -742,3 +742,35 @@ void orc_eventlog_record(uint64_t seq, uint32_t slot, const orc_tile* t, uint32_
     put_le(out, &o, version == 2 ? orc_record_checksum(seq, slot, tb) : 0u, 4);
     memcpy(out + o, tb, 128);
 }
+
+/* ------------------------------------------------------------------------ */
+/* CCOS observe_scores (ccos.rs:257-300), sequential f32 as the reference. */
+
+void orc_observe_scores(const uint32_t* slots, const float* scores, size_t n, const uint8_t* live,
+                        size_t n_slots, float temperature, float* importance) {
+    if (n == 0 || !isfinite(temperature) || temperature <= 0.0f) return;
+    size_t n_live = 0;
+    float m = -INFINITY;
+    for (size_t i = 0; i < n; ++i) {
+        if (slots[i] >= n_slots || !live[slots[i]]) continue;
+        if (!isfinite(scores[i])) return;
+        ++n_live;
+        m = fmaxf(m, scores[i]);
+    }
+    if (n_live == 0) return;
+    float sum = 0.0f;
+    float* w = (float*)malloc(n * sizeof(float));
+    if (!w) return;
+    for (size_t i = 0; i < n; ++i) {
+        w[i] = 0.0f;
+        if (slots[i] >= n_slots || !live[slots[i]]) continue;
+        w[i] = expf((scores[i] - m) / temperature);
+        sum += w[i];
+    }
+    if (isfinite(sum) && sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (size_t i = 0; i < n; ++i)
+            if (slots[i] < n_slots && live[slots[i]]) importance[slots[i]] += w[i] * inv;
+    }
+    free(w);
+}

@@ -139,6 +139,13 @@ uint32_t orc_record_checksum(uint64_t seq, uint32_t slot, const uint8_t* tile_by
 void orc_eventlog_record(uint64_t seq, uint32_t slot, const orc_tile* t, uint32_t version,
                          uint8_t* out);
 
+/* ccos.rs:257-300 — observe_scores: H2O importance from (slot, score) pairs.
+ * live[slot] != 0 for a HOT/WARM slot; slots >= n_slots or not live are
+ * skipped; no update when no pair is live, a live score is non-finite, the
+ * temperature is non-finite or <= 0, or the f32 sum is not finite and > 0. */
+void orc_observe_scores(const uint32_t* slots, const float* scores, size_t n, const uint8_t* live,
+                        size_t n_slots, float temperature, float* importance);
+
 /* Batched helpers for tests (row-major inputs, one tile per key). */
 int orc_encode_batch(const float* keys, size_t n, int codec, int residual_mode, const float* z,
                      const float* rht_diag, uint32_t pos0, uint16_t head_id, orc_tile* out);

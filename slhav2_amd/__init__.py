@@ -137,6 +137,18 @@ _SIGS = {
     "slha_eventlog_close": (_I32, [_P]),
     "slha_gpu_eventlog_pack": (_I32, [_P, _P, _P, _SZ, _U32, _P, _P]),
     "slha_gpu_eventlog_unpack": (_I32, [_P, _SZ, _U32, _P, _P, _P, _P]),
+    "slha_ccos_new": (_P, [_P, _SZ, _SZ, _I32, _I32, _SZ]),
+    "slha_ccos_free": (_I32, [_P]),
+    "slha_ccos_attach_event_log": (_I32, [_P, _P, _I32]),
+    "slha_ccos_insert": (_I32, [_P, _P, _SZ, _P, _P]),
+    "slha_ccos_observe_scores": (_I32, [_P, _P, _SZ, ctypes.c_float, _P]),
+    "slha_ccos_enforce_budget": (_I32, [_P, _P, _P]),
+    "slha_ccos_page_out": (_I32, [_P, _U32, _P]),
+    "slha_ccos_drop_correction": (_I32, [_P, _U32, _P, _P]),
+    "slha_ccos_evict": (_I32, [_P, _U32, _P, _P]),
+    "slha_ccos_rehydrate": (_I32, [_P, _U64, _P, _P]),
+    "slha_ccos_stats": (_I32, [_P, _P]),
+    "slha_ccos_slots": (_I32, [_P, _SZ, _P, _P, _P, _P]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -631,3 +643,159 @@ def gpu_eventlog_unpack(records, dst_slots, arena, version: int = 2, stream=None
     _check(lib.slha_gpu_eventlog_unpack(_dev_ptr(records), n, version, _dev_ptr(dst_slots),
                                         _dev_ptr(arena.reshape(-1, 128)), _dev_ptr(status), _stream(stream)))
     return status
+
+
+# ---------------------------------------------------------------------------
+# CCOS ElasticKvCache (scirust/src/ccos.rs) over a device arena
+
+PAGE_LOWEST_IMPACT_FIRST, PAGE_OLDEST_FIRST = 0, 1
+EVICT_CAUSAL, EVICT_IMPORTANCE = 0, 1
+HOT, WARM, COLD = 0, 1, 2
+
+
+class _CcosStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("live_bytes", "len", "hot", "warm", "cold", "nocorr",
+                                                "reclaimed_correction", "log_errors", "blocked_evictions")]
+
+
+class ElasticKvCache:
+    """Mirror of `ElasticKvCache` (ccos.rs:105-614) with the arena in HBM:
+    `arena` is a uint8 GPU tensor [capacity, 128] that the cache fills from
+    slot 0. Method names follow the reference; scores come from the GPU."""
+
+    def __init__(self, arena, budget_bytes: int, policy: int = PAGE_LOWEST_IMPACT_FIRST,
+                 eviction: int = EVICT_CAUSAL, sink_window: int = 0, stream=None):
+        self.arena = arena.reshape(-1, 128)
+        self._stream = stream
+        self._log = None
+        h = lib.slha_ccos_new(_dev_ptr(self.arena), self.arena.shape[0], budget_bytes, policy, eviction,
+                              sink_window)
+        if not h:
+            raise SlhaError(ERR_DIMENSION, last_error())
+        self._h = h
+
+    @classmethod
+    def with_budget(cls, arena, budget_bytes: int, **kw) -> "ElasticKvCache":
+        return cls(arena, budget_bytes, **kw)
+
+    @classmethod
+    def with_eviction(cls, arena, budget_bytes: int, sink_window: int | None = None, **kw):
+        """EvictionPolicy::Importance { sink_window } when sink_window is given."""
+        if sink_window is None:
+            return cls(arena, budget_bytes, **kw)
+        return cls(arena, budget_bytes, eviction=EVICT_IMPORTANCE, sink_window=sink_window, **kw)
+
+    def close(self) -> None:
+        if self._h:
+            _check(lib.slha_ccos_free(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attach_event_log(self, log: "EventLog") -> None:
+        self._log = log
+        _check(lib.slha_ccos_attach_event_log(self._h, log._h, 0))
+
+    def attach_durable_event_log(self, log: "EventLog") -> None:
+        self._log = log
+        _check(lib.slha_ccos_attach_event_log(self._h, log._h, 1))
+
+    def insert(self, tiles) -> list:
+        """Inserts GPU tiles (uint8 [n, 128]) in order; returns their slots."""
+        import numpy as np
+
+        t = tiles.reshape(-1, 128)
+        out = np.zeros(t.shape[0], np.uint32)
+        _check(lib.slha_ccos_insert(self._h, _dev_ptr(t), t.shape[0], out.ctypes.data, _stream(self._stream)))
+        return [int(x) for x in out]
+
+    def _stats(self) -> _CcosStats:
+        st = _CcosStats()
+        _check(lib.slha_ccos_stats(self._h, ctypes.byref(st)))
+        return st
+
+    def __len__(self) -> int:
+        return self._stats().len
+
+    def live_bytes(self) -> int:
+        return self._stats().live_bytes
+
+    def counts(self) -> tuple:
+        st = self._stats()
+        return st.hot, st.warm, st.cold
+
+    def nocorr_count(self) -> int:
+        return self._stats().nocorr
+
+    def reclaimed_correction_bytes(self) -> int:
+        return self._stats().reclaimed_correction
+
+    def log_errors(self) -> int:
+        return self._stats().log_errors
+
+    def blocked_evictions(self) -> int:
+        return self._stats().blocked_evictions
+
+    def _slots(self):
+        import numpy as np
+
+        n = len(self)
+        state = np.zeros(n, np.int32)
+        seq = np.zeros(n, np.uint64)
+        imp = np.zeros(n, np.float32)
+        _check(lib.slha_ccos_slots(self._h, n, state.ctypes.data, seq.ctypes.data, imp.ctypes.data,
+                                   _stream(self._stream)))
+        return state, seq, imp
+
+    def state(self, slot: int) -> int:
+        return int(self._slots()[0][slot])
+
+    def importance(self, slot: int) -> float:
+        return float(self._slots()[2][slot])
+
+    def tile(self, slot: int):
+        return self.arena[slot]
+
+    def score_all(self, q_coarse, q_sign):
+        """(slots, scores) of every live slot, scored on the GPU in exact mode
+        (compute_score, tile.rs:267-281); also returns the dense score row."""
+        import numpy as np
+
+        n = len(self)
+        dense = gpu_score(self.arena[:n], q_coarse.reshape(1, -1), q_sign.reshape(1, -1), group=1,
+                          mode=SCORE_EXACT, stream=self._stream).reshape(-1)
+        state = self._slots()[0]
+        live = np.nonzero(state != COLD)[0]
+        return live, dense.cpu().numpy()[live], dense
+
+    def observe_scores(self, scores, temperature: float) -> None:
+        """scores: f32 GPU tensor of the arena prefix (one per slot)."""
+        _check(lib.slha_ccos_observe_scores(self._h, _dev_ptr(scores), scores.numel(), temperature,
+                                            _stream(self._stream)))
+
+    def enforce_budget(self) -> bool:
+        ok = ctypes.c_int32(0)
+        _check(lib.slha_ccos_enforce_budget(self._h, ctypes.byref(ok), _stream(self._stream)))
+        return bool(ok.value)
+
+    def page_out(self, slot: int) -> None:
+        _check(lib.slha_ccos_page_out(self._h, slot, _stream(self._stream)))
+
+    def drop_correction(self, slot: int) -> bool:
+        done = ctypes.c_int32(0)
+        _check(lib.slha_ccos_drop_correction(self._h, slot, ctypes.byref(done), _stream(self._stream)))
+        return bool(done.value)
+
+    def evict(self, slot: int) -> bool:
+        done = ctypes.c_int32(0)
+        _check(lib.slha_ccos_evict(self._h, slot, ctypes.byref(done), _stream(self._stream)))
+        return bool(done.value)
+
+    def rehydrate(self, seq: int):
+        slot = ctypes.c_int64(-1)
+        _check(lib.slha_ccos_rehydrate(self._h, seq, ctypes.byref(slot), _stream(self._stream)))
+        return None if slot.value < 0 else int(slot.value)

@@ -15,6 +15,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cerrno>
 #include <cmath>
 #include <cstdarg>
@@ -29,6 +30,7 @@
 #include <vector>
 
 #include "../../include/slha.h"
+#include "../../include/slha_ccos.h"
 #include "../../include/slha_eventlog.h"
 #include "../../include/slha_gpu.h"
 #include "slha_launch.h"
@@ -1412,6 +1414,470 @@ int32_t slha_gpu_eventlog_unpack(const uint8_t* records_dev, size_t n, uint32_t 
         check_hip(launch_eventlog_unpack(records_dev, n, version, dst_slots_dev, arena_dev, status_dev,
                                          static_cast<hipStream_t>(stream)),
                   "eventlog unpack kernel");
+    });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// CCOS ElasticKvCache (scirust/src/ccos.rs) over a device arena: the control
+// plane on the host, the byte changes and the importance on the device.
+
+namespace {
+
+constexpr uint8_t kHot = SLHA_CCOS_HOT, kWarm = SLHA_CCOS_WARM, kCold = SLHA_CCOS_COLD;
+constexpr uint64_t kHotBytes = 128, kWarmBytes = 96;  // ccos.rs:32-34
+
+struct DevBuf {  // grow-only device staging
+    void* p = nullptr;
+    size_t cap = 0;
+    void* get(size_t bytes) {
+        if (bytes > cap) {
+            if (p) (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+            check_hip(hipMalloc(&p, bytes), "hipMalloc (CCOS staging)");
+            cap = bytes;
+        }
+        return p;
+    }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+struct CcosObj {
+    uint4* arena = nullptr;
+    uint64_t capacity = 0, budget = 0, sink_window = 0;
+    int page_policy = 0, evict_policy = 0;
+    // host mirror, per slot of the arena prefix
+    std::vector<uint8_t> state;
+    std::vector<uint64_t> seq;
+    std::vector<float> sigma;
+    std::vector<uint32_t> position;
+    std::vector<uint16_t> flags;
+    std::vector<uint32_t> free_list;
+    uint64_t live = 0, next_seq = 0, log_errors = 0, blocked = 0;
+    SlhaEventLog* log = nullptr;
+    bool durable = false;
+    // device
+    float* importance = nullptr;
+    uint8_t* state_dev = nullptr;
+    float* obs_ws = nullptr;
+    DevBuf stage_a, stage_b, stage_c;
+    ~CcosObj() {
+        if (importance) (void)hipFree(importance);
+        if (state_dev) (void)hipFree(state_dev);
+        if (obs_ws) (void)hipFree(obs_ws);
+    }
+    uint64_t len() const { return state.size(); }
+    uint64_t sep_bytes(uint64_t s) const {  // tile.rs:120-128
+        return (flags[s] & SLHA_FLAG_TQ3) ? 16 : ((flags[s] & SLHA_FLAG_MIX3) ? 14 : 0);
+    }
+    uint64_t slot_live_bytes(uint64_t s) const {  // ccos.rs:470-482
+        if (state[s] == kCold) return 0;
+        const uint64_t base = state[s] == kHot ? kHotBytes : kWarmBytes;
+        return base - ((flags[s] & SLHA_FLAG_TQ3_NOCORR) ? sep_bytes(s) : 0);
+    }
+};
+
+struct CcosRegistry {
+    std::mutex mu;
+    std::unordered_map<uintptr_t, std::unique_ptr<CcosObj>> live;
+};
+
+CcosRegistry& ccos_registry() {
+    static CcosRegistry* r = new CcosRegistry();
+    return *r;
+}
+
+CcosObj* ccos_of(const SlhaCcos* c) {
+    if (!c) fail(SLHA_ERR_NULL, "CCOS handle is NULL");
+    auto& r = ccos_registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    auto it = r.live.find(reinterpret_cast<uintptr_t>(c));
+    if (it == r.live.end()) fail(SLHA_ERR_INVALID_HANDLE, "CCOS handle is not a live SLHA handle");
+    return it->second.get();
+}
+
+// f32::total_cmp as a signed integer key.
+int32_t total_key(float f) {
+    int32_t k;
+    std::memcpy(&k, &f, 4);
+    return k ^ (int32_t)((uint32_t)(k >> 31) >> 1);
+}
+
+template <class T>
+T* stage(DevBuf& b, const T* host, size_t n, hipStream_t s) {
+    T* d = static_cast<T*>(b.get(std::max<size_t>(n, 1) * sizeof(T)));
+    check_hip(hipMemcpyAsync(d, host, n * sizeof(T), hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+    return d;
+}
+
+void sync_state(CcosObj* C, hipStream_t s) {
+    if (C->len() == 0) return;
+    check_hip(hipMemcpyAsync(C->state_dev, C->state.data(), C->len(), hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync (CCOS state)");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// ccos.rs:497-512
+std::vector<uint32_t> paging_order(const CcosObj* C, uint8_t st) {
+    std::vector<uint32_t> v;
+    for (uint64_t s = 0; s < C->len(); ++s)
+        if (C->state[s] == st) v.push_back((uint32_t)s);
+    if (C->page_policy == SLHA_CCOS_PAGE_LOWEST_IMPACT_FIRST)
+        std::stable_sort(v.begin(), v.end(), [&](uint32_t a, uint32_t b) {
+            return total_key(C->sigma[a]) < total_key(C->sigma[b]);
+        });
+    else
+        std::stable_sort(v.begin(), v.end(), [&](uint32_t a, uint32_t b) { return C->seq[a] < C->seq[b]; });
+    return v;
+}
+
+void apply_op(CcosObj* C, const std::vector<uint32_t>& slots, int op, hipStream_t s) {
+    if (slots.empty()) return;
+    const uint32_t* d = stage(C->stage_a, slots.data(), slots.size(), s);
+    check_hip(launch_ccos_apply(C->arena, d, slots.size(), op, s), "ccos kernel");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// drop_correction's host effect (ccos.rs:386-397); true when bytes were reclaimed.
+bool drop_corr_host(CcosObj* C, uint32_t s) {
+    const uint64_t n = C->sep_bytes(s);
+    if (C->state[s] == kCold || n == 0 || (C->flags[s] & SLHA_FLAG_TQ3_NOCORR)) return false;
+    C->flags[s] |= SLHA_FLAG_TQ3_NOCORR;
+    C->live -= n;
+    return true;
+}
+
+// page_out's host effect (ccos.rs:369-378).
+bool page_out_host(CcosObj* C, uint32_t s) {
+    if (C->state[s] != kHot) return false;
+    C->live -= C->slot_live_bytes(s);
+    C->flags[s] |= SLHA_FLAG_WARM;
+    C->state[s] = kWarm;
+    C->live += C->slot_live_bytes(s);
+    return true;
+}
+
+// evict (ccos.rs:404-438) of a batch, in order: the records go to the log in
+// one append; a failed durable append keeps the whole batch live. Returns the
+// number of slots that became COLD.
+size_t evict_batch(CcosObj* C, const std::vector<uint32_t>& slots, hipStream_t s) {
+    if (slots.empty()) return 0;
+    const size_t n = slots.size();
+    if (C->log) {
+        std::vector<uint64_t> seqs(n);
+        for (size_t i = 0; i < n; ++i) seqs[i] = C->seq[slots[i]];
+        const uint32_t* ds = stage(C->stage_a, slots.data(), n, s);
+        const uint64_t* dq = stage(C->stage_b, seqs.data(), n, s);
+        void* dr = C->stage_c.get(n * SLHA_EVENTLOG_RECORD_BYTES);
+        const uint32_t version = slha_eventlog_version(C->log);
+        if (version == 0) fail(SLHA_ERR_INVALID_HANDLE, "attached EventLog handle is no longer live");
+        check_hip(launch_eventlog_pack(C->arena, ds, dq, n, version, dr, s), "eventlog pack kernel");
+        std::vector<uint8_t> rec(n * SLHA_EVENTLOG_RECORD_BYTES);
+        check_hip(hipMemcpyAsync(rec.data(), dr, rec.size(), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        const int32_t rc = slha_eventlog_append(C->log, rec.data(), n, C->durable ? 1 : 0);
+        if (rc != SLHA_OK) {
+            C->log_errors += n;
+            if (C->durable) {
+                C->blocked += n;
+                return 0;
+            }
+        }
+    } else if (C->durable) {
+        C->blocked += n;
+        return 0;
+    }
+    for (uint32_t sl : slots) {
+        C->live -= C->slot_live_bytes(sl);
+        C->state[sl] = kCold;
+        C->free_list.push_back(sl);
+    }
+    return n;
+}
+
+// insert_with_state (ccos.rs:226-247) of tiles already read to the host;
+// returns the slots.
+std::vector<uint32_t> insert_host(CcosObj* C, const uint8_t* tiles, size_t n) {
+    uint64_t fresh = 0;
+    const uint64_t reuse = std::min<uint64_t>(n, C->free_list.size());
+    fresh = n - reuse;
+    if (C->len() + fresh > C->capacity)
+        fail(SLHA_ERR_DIMENSION, "CCOS arena full: %llu slots in use, %zu tiles to insert, capacity %llu",
+             (unsigned long long)C->len(), n, (unsigned long long)C->capacity);
+    std::vector<uint32_t> slots(n);
+    for (size_t i = 0; i < n; ++i) {
+        const uint8_t* t = tiles + 128 * i;
+        float sg;
+        std::memcpy(&sg, t + 104, 4);
+        uint32_t pos;
+        std::memcpy(&pos, t + 112, 4);
+        uint16_t fl;
+        std::memcpy(&fl, t + 118, 2);
+        uint32_t sl;
+        if (!C->free_list.empty()) {
+            sl = C->free_list.back();
+            C->free_list.pop_back();
+        } else {
+            sl = (uint32_t)C->len();
+            C->state.push_back(kCold);
+            C->seq.push_back(0);
+            C->sigma.push_back(0.0f);
+            C->position.push_back(0);
+            C->flags.push_back(0);
+        }
+        C->state[sl] = (fl & SLHA_FLAG_WARM) ? kWarm : kHot;
+        C->seq[sl] = C->next_seq++;
+        C->sigma[sl] = sg;
+        C->position[sl] = pos;
+        C->flags[sl] = fl;
+        C->live += C->slot_live_bytes(sl);
+        slots[i] = sl;
+    }
+    return slots;
+}
+
+}  // namespace
+
+extern "C" {
+
+SlhaCcos* slha_ccos_new(SciRustSlhaTile* arena_dev, size_t capacity, size_t budget_bytes,
+                        int32_t page_policy, int32_t eviction_policy, size_t sink_window) {
+    SlhaCcos* out = nullptr;
+    const int32_t rc = ffi_status([&] {
+        if (!arena_dev) fail(SLHA_ERR_NULL, "slha_ccos_new received a NULL arena");
+        if (capacity == 0 || capacity > 0xFFFFFFFFull) fail(SLHA_ERR_DIMENSION, "capacity=%zu out of range", capacity);
+        if (page_policy != SLHA_CCOS_PAGE_LOWEST_IMPACT_FIRST && page_policy != SLHA_CCOS_PAGE_OLDEST_FIRST)
+            fail(SLHA_ERR_DIMENSION, "unknown page-out policy %d", page_policy);
+        if (eviction_policy != SLHA_CCOS_EVICT_CAUSAL && eviction_policy != SLHA_CCOS_EVICT_IMPORTANCE)
+            fail(SLHA_ERR_DIMENSION, "unknown eviction policy %d", eviction_policy);
+        require_device();
+        auto C = std::make_unique<CcosObj>();
+        C->arena = reinterpret_cast<uint4*>(arena_dev);
+        C->capacity = capacity;
+        C->budget = budget_bytes;
+        C->page_policy = page_policy;
+        C->evict_policy = eviction_policy;
+        C->sink_window = sink_window;
+        check_hip(hipMalloc(reinterpret_cast<void**>(&C->importance), capacity * sizeof(float)), "hipMalloc");
+        check_hip(hipMalloc(reinterpret_cast<void**>(&C->state_dev), capacity), "hipMalloc");
+        check_hip(hipMalloc(reinterpret_cast<void**>(&C->obs_ws), observe_workspace_floats() * sizeof(float)),
+                  "hipMalloc");
+        SlhaCcos* token = reinterpret_cast<SlhaCcos*>(new uint64_t(0));
+        auto& r = ccos_registry();
+        std::lock_guard<std::mutex> lock(r.mu);
+        r.live.emplace(reinterpret_cast<uintptr_t>(token), std::move(C));
+        out = token;
+    });
+    return rc == SLHA_OK ? out : nullptr;
+}
+
+int32_t slha_ccos_free(SlhaCcos* c) {
+    return ffi_status([&] {
+        if (!c) fail(SLHA_ERR_NULL, "CCOS handle is NULL");
+        std::unique_ptr<CcosObj> obj;
+        auto& r = ccos_registry();
+        {
+            std::lock_guard<std::mutex> lock(r.mu);
+            auto it = r.live.find(reinterpret_cast<uintptr_t>(c));
+            if (it == r.live.end()) fail(SLHA_ERR_INVALID_HANDLE, "CCOS handle is not a live SLHA handle");
+            obj = std::move(it->second);
+            r.live.erase(it);
+        }
+    });
+}
+
+int32_t slha_ccos_attach_event_log(SlhaCcos* c, SlhaEventLog* log, int32_t durable) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (log) (void)log_of(log);
+        C->log = log;
+        C->durable = log && durable;
+    });
+}
+
+int32_t slha_ccos_insert(SlhaCcos* c, const SciRustSlhaTile* tiles_dev, size_t n, uint32_t* slots_out,
+                         void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (n == 0) return;
+        if (!tiles_dev || !slots_out) fail(SLHA_ERR_NULL, "slha_ccos_insert received a NULL pointer");
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        std::vector<uint8_t> host(n * 128);
+        check_hip(hipMemcpyAsync(host.data(), tiles_dev, host.size(), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        const std::vector<uint32_t> slots = insert_host(C, host.data(), n);
+        const uint32_t* d = stage(C->stage_a, slots.data(), n, s);
+        check_hip(launch_tile_scatter(tiles_dev, d, n, C->arena, C->importance, s), "tile scatter kernel");
+        sync_state(C, s);
+        std::memcpy(slots_out, slots.data(), n * sizeof(uint32_t));
+    });
+}
+
+int32_t slha_ccos_observe_scores(SlhaCcos* c, const float* scores_dev, size_t n, float temperature,
+                                 void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (n > C->len()) fail(SLHA_ERR_DIMENSION, "n=%zu scores for %llu slots", n, (unsigned long long)C->len());
+        if (n == 0 || !std::isfinite(temperature) || temperature <= 0.0f) return;
+        if (!scores_dev) fail(SLHA_ERR_NULL, "slha_ccos_observe_scores received a NULL pointer");
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        check_hip(launch_observe_scores(scores_dev, C->state_dev, n, temperature, C->importance, C->obs_ws, s),
+                  "observe kernels");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    });
+}
+
+int32_t slha_ccos_enforce_budget(SlhaCcos* c, int32_t* within_out, void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        auto within = [&] { return C->live <= C->budget; };
+        auto finish = [&] {
+            sync_state(C, s);
+            if (within_out) *within_out = within() ? 1 : 0;
+        };
+        if (within()) return finish();
+        // Phases 1-3 (ccos.rs:533-563): the host takes each rung in order while
+        // over budget; each phase's tiles change in one launch.
+        const struct {
+            uint8_t st;
+            int op;
+        } phases[3] = {{kHot, 1}, {kHot, 0}, {kWarm, 1}};
+        for (const auto& ph : phases) {
+            std::vector<uint32_t> batch;
+            for (uint32_t sl : paging_order(C, ph.st)) {
+                if (within()) break;
+                if (ph.op == 1 ? drop_corr_host(C, sl) : page_out_host(C, sl)) batch.push_back(sl);
+            }
+            apply_op(C, batch, ph.op, s);
+            if (within()) return finish();
+        }
+        // Phase 4 (ccos.rs:565-613): eviction order.
+        std::vector<uint32_t> live;
+        for (uint64_t sl = 0; sl < C->len(); ++sl)
+            if (C->state[sl] != kCold) live.push_back((uint32_t)sl);
+        if (C->evict_policy == SLHA_CCOS_EVICT_CAUSAL) {
+            std::stable_sort(live.begin(), live.end(), [&](uint32_t a, uint32_t b) { return C->seq[a] < C->seq[b]; });
+        } else {
+            std::vector<float> imp(C->len());
+            check_hip(hipMemcpyAsync(imp.data(), C->importance, imp.size() * 4, hipMemcpyDeviceToHost, s),
+                      "hipMemcpyAsync");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            const uint64_t sw = (uint32_t)C->sink_window;  // `sink_window as u32`
+            std::stable_sort(live.begin(), live.end(), [&](uint32_t a, uint32_t b) {
+                const bool sa = C->position[a] < sw, sb = C->position[b] < sw;
+                if (sa != sb) return !sa;
+                const int32_t ka = total_key(imp[a]), kb = total_key(imp[b]);
+                if (ka != kb) return ka < kb;
+                return C->seq[a] < C->seq[b];
+            });
+        }
+        // The prefix whose eviction reaches the budget, evicted as one batch.
+        std::vector<uint32_t> batch;
+        uint64_t after = C->live;
+        for (uint32_t sl : live) {
+            if (after <= C->budget) break;
+            after -= C->slot_live_bytes(sl);
+            batch.push_back(sl);
+        }
+        evict_batch(C, batch, s);
+        finish();
+    });
+}
+
+int32_t slha_ccos_page_out(SlhaCcos* c, uint32_t slot, void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (slot >= C->len()) fail(SLHA_ERR_DIMENSION, "slot %u out of range", slot);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (page_out_host(C, slot)) apply_op(C, {slot}, 0, s);
+        sync_state(C, s);
+    });
+}
+
+int32_t slha_ccos_drop_correction(SlhaCcos* c, uint32_t slot, int32_t* done_out, void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (slot >= C->len()) fail(SLHA_ERR_DIMENSION, "slot %u out of range", slot);
+        const bool done = drop_corr_host(C, slot);
+        if (done) apply_op(C, {slot}, 1, static_cast<hipStream_t>(stream));
+        if (done_out) *done_out = done ? 1 : 0;
+    });
+}
+
+int32_t slha_ccos_evict(SlhaCcos* c, uint32_t slot, int32_t* done_out, void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        size_t done = 0;
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (slot < C->len() && C->state[slot] != kCold) done = evict_batch(C, {slot}, s);
+        sync_state(C, s);
+        if (done_out) *done_out = done ? 1 : 0;
+    });
+}
+
+int32_t slha_ccos_rehydrate(SlhaCcos* c, uint64_t seq, int64_t* slot_out, void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (!slot_out) fail(SLHA_ERR_NULL, "slha_ccos_rehydrate received a NULL pointer");
+        *slot_out = -1;
+        if (!C->log) return;
+        uint64_t idx = 0;
+        int32_t found = 0;
+        if (slha_eventlog_find_seq(C->log, seq, &idx, &found) != SLHA_OK)
+            fail(SLHA_ERR_IO, "%s", slha_last_error_message());
+        if (!found) return;
+        uint8_t rec[SLHA_EVENTLOG_RECORD_BYTES];
+        if (slha_eventlog_read(C->log, idx, 1, rec) != SLHA_OK) fail(SLHA_ERR_IO, "%s", slha_last_error_message());
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        const std::vector<uint32_t> slots = insert_host(C, rec + 16, 1);
+        const uint8_t* dt = stage(C->stage_b, rec + 16, 128, s);
+        const uint32_t* d = stage(C->stage_a, slots.data(), 1, s);
+        check_hip(launch_tile_scatter(dt, d, 1, C->arena, C->importance, s), "tile scatter kernel");
+        sync_state(C, s);
+        *slot_out = slots[0];
+    });
+}
+
+int32_t slha_ccos_stats(const SlhaCcos* c, SlhaCcosStats* out) {
+    return ffi_status([&] {
+        const CcosObj* C = ccos_of(c);
+        if (!out) fail(SLHA_ERR_NULL, "slha_ccos_stats received a NULL pointer");
+        SlhaCcosStats st{};
+        st.live_bytes = C->live;
+        st.len = C->len();
+        for (uint64_t sl = 0; sl < C->len(); ++sl) {
+            const uint8_t x = C->state[sl];
+            (x == kHot ? st.hot : x == kWarm ? st.warm : st.cold) += 1;
+            if (x != kCold && (C->flags[sl] & SLHA_FLAG_TQ3_NOCORR)) {
+                st.nocorr += 1;
+                st.reclaimed_correction += C->sep_bytes(sl);
+            }
+        }
+        st.log_errors = C->log_errors;
+        st.blocked_evictions = C->blocked;
+        *out = st;
+    });
+}
+
+int32_t slha_ccos_slots(SlhaCcos* c, size_t n, int32_t* state_out, uint64_t* seq_out, float* importance_out,
+                        void* stream) {
+    return ffi_status([&] {
+        CcosObj* C = ccos_of(c);
+        if (n > C->len()) fail(SLHA_ERR_DIMENSION, "n=%zu exceeds %llu slots", n, (unsigned long long)C->len());
+        for (size_t i = 0; i < n; ++i) {
+            if (state_out) state_out[i] = C->state[i];
+            if (seq_out) seq_out[i] = C->seq[i];
+        }
+        if (importance_out && n) {
+            const hipStream_t s = static_cast<hipStream_t>(stream);
+            check_hip(hipMemcpyAsync(importance_out, C->importance, n * 4, hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        }
     });
 }
 

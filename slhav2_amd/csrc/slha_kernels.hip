@@ -14,6 +14,7 @@
 //   learned_*_kernel       d > 128 LearnedModel encode / query / decode (learned.rs:257-408)
 //   attn_*_kernel          decode attention softmax(s * scale) . V (benchmark_decode.rs:29-90)
 //   eventlog_*_kernel      EventLog records of evicted tiles, and rehydrate (eventlog.rs:9-36)
+//   observe_*_kernel       CCOS H2O importance from the arena's scores (ccos.rs:257-300)
 #include "slha_device.h"
 #include "slha_launch.h"
 
@@ -3001,6 +3002,106 @@ __global__ __launch_bounds__(256) void eventlog_unpack_kernel(const uint4* __res
 }
 
 // ---------------------------------------------------------------------------
+// CCOS control plane over the device arena (ccos.rs)
+
+// insert: tile i -> arena slot dst[i] with 8 lanes per tile, importance reset.
+__global__ __launch_bounds__(256) void tile_scatter_kernel(const uint4* __restrict__ src,
+                                                           const uint32_t* __restrict__ dst,
+                                                           uint64_t n, uint4* __restrict__ arena,
+                                                           float* __restrict__ importance) {
+    const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (q >= n * 8) return;
+    const uint64_t i = q >> 3;
+    const uint32_t j = (uint32_t)(q & 7u);
+    const uint32_t slot = dst[i];
+    arena[(size_t)slot * 8 + j] = src[q];
+    if (j == 0 && importance) importance[slot] = 0.0f;
+}
+
+// observe_scores (ccos.rs:257-300) over the scores of slots [0, n), in three
+// launches with fixed reduction orders (so repeated calls agree bit for bit):
+//   1. per workgroup: max of the live scores and a non-finite flag;
+//   2. per workgroup: M = max of pass 1, then sum of exp((s - M) / T);
+//   3. every workgroup: L = sum of pass 2 (same order), then, when the
+//      inputs are valid, importance[s] += exp((s - M) / T) * (1 / L).
+// partial holds 2 * kObsBlocks floats; grid = min(blocks needed, kObsBlocks).
+constexpr uint32_t kObsBlocks = 1024;
+
+__device__ __forceinline__ float block_reduce_f(float x, bool is_max, float* tmp) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float y = __shfl_xor(x, o);
+        x = is_max ? fmaxf(x, y) : x + y;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0) tmp[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return is_max ? fmaxf(fmaxf(tmp[0], tmp[1]), fmaxf(tmp[2], tmp[3])) : (tmp[0] + tmp[1]) + (tmp[2] + tmp[3]);
+}
+
+// Reduces the first `count` entries of v (count <= kObsBlocks) in a fixed order.
+__device__ __forceinline__ float reduce_partials(const float* v, uint32_t count, bool is_max, float* tmp) {
+    float x = is_max ? -INFINITY : 0.0f;
+    for (uint32_t k = threadIdx.x; k < count; k += 256u) x = is_max ? fmaxf(x, v[k]) : x + v[k];
+    return block_reduce_f(x, is_max, tmp);
+}
+
+__global__ __launch_bounds__(256) void observe_max_kernel(const float* __restrict__ scores,
+                                                          const uint8_t* __restrict__ state, uint64_t n,
+                                                          float* __restrict__ partial) {
+    __shared__ float tmp[4];
+    float m = -INFINITY, bad = 0.0f, live = 0.0f;
+    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
+        if (state[s] == 2) continue;  // COLD
+        const float x = scores[s];
+        live = 1.0f;
+        if (!isfinite(x)) bad = 1.0f;
+        else m = fmaxf(m, x);
+    }
+    m = block_reduce_f(m, true, tmp);
+    bad = block_reduce_f(bad, true, tmp);
+    live = block_reduce_f(live, true, tmp);
+    if (threadIdx.x == 0) {
+        partial[blockIdx.x] = m;
+        // a non-finite live score poisons the max so pass 3 skips the update
+        partial[kObsBlocks + blockIdx.x] = bad != 0.0f ? 1.0f : (live != 0.0f ? 0.0f : -1.0f);
+    }
+}
+
+__global__ __launch_bounds__(256) void observe_sum_kernel(const float* __restrict__ scores,
+                                                          const uint8_t* __restrict__ state, uint64_t n,
+                                                          float temperature, float* __restrict__ partial,
+                                                          float* __restrict__ partial_sum) {
+    __shared__ float tmp[4];
+    const float M = reduce_partials(partial, gridDim.x, true, tmp);
+    float acc = 0.0f;
+    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
+        if (state[s] == 2) continue;
+        const float x = scores[s];
+        if (isfinite(x)) acc += expf((x - M) / temperature);
+    }
+    acc = block_reduce_f(acc, false, tmp);
+    if (threadIdx.x == 0) partial_sum[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restrict__ scores,
+                                                            const uint8_t* __restrict__ state, uint64_t n,
+                                                            float temperature, const float* __restrict__ partial,
+                                                            const float* __restrict__ partial_sum,
+                                                            float* __restrict__ importance) {
+    __shared__ float tmp[4];
+    const float M = reduce_partials(partial, gridDim.x, true, tmp);
+    const float flag = reduce_partials(partial + kObsBlocks, gridDim.x, true, tmp);  // 1 bad, 0 ok, -1 no live
+    const float L = reduce_partials(partial_sum, gridDim.x, false, tmp);
+    if (flag != 0.0f || !isfinite(L) || !(L > 0.0f)) return;
+    const float inv = 1.0f / L;
+    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
+        if (state[s] == 2) continue;
+        importance[s] += expf((scores[s] - M) / temperature) * inv;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Launchers
 
 size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
@@ -3380,6 +3481,29 @@ hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t vers
     if (n == 0) return hipSuccess;
     eventlog_unpack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
         static_cast<const uint4*>(records), n, version, dst, static_cast<uint4*>(arena), status);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_scatter(const void* src, const uint32_t* dst, uint64_t n, void* arena,
+                               float* importance, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    tile_scatter_kernel<<<(unsigned)((n * 8 + 255) / 256), 256, 0, s>>>(
+        static_cast<const uint4*>(src), dst, n, static_cast<uint4*>(arena), importance);
+    return hipGetLastError();
+}
+
+size_t observe_workspace_floats() { return 3 * (size_t)kObsBlocks; }
+
+hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint64_t n, float temperature,
+                                 float* importance, float* workspace, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint64_t need = (n + 1023) / 1024;
+    const unsigned blocks = (unsigned)(need < kObsBlocks ? need : kObsBlocks);
+    float* partial = workspace;                   // [max | flag] x kObsBlocks
+    float* partial_sum = workspace + 2 * kObsBlocks;
+    observe_max_kernel<<<blocks, 256, 0, s>>>(scores, state, n, partial);
+    observe_sum_kernel<<<blocks, 256, 0, s>>>(scores, state, n, temperature, partial, partial_sum);
+    observe_apply_kernel<<<blocks, 256, 0, s>>>(scores, state, n, temperature, partial, partial_sum, importance);
     return hipGetLastError();
 }
 

@@ -98,6 +98,14 @@ hipError_t launch_eventlog_pack(const void* arena, const uint32_t* slots, const 
                                 uint64_t n, uint32_t version, void* records, hipStream_t s);
 hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t version,
                                   const uint32_t* dst, void* arena, uint32_t* status, hipStream_t s);
+// CCOS: tile i -> arena slot dst[i] (importance[dst[i]] = 0 when non-NULL);
+// observe_scores over scores[0, n) with state (0 HOT, 1 WARM, 2 COLD) and a
+// workspace of observe_workspace_floats() floats.
+hipError_t launch_tile_scatter(const void* src, const uint32_t* dst, uint64_t n, void* arena,
+                               float* importance, hipStream_t s);
+size_t observe_workspace_floats();
+hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint64_t n, float temperature,
+                                 float* importance, float* workspace, hipStream_t s);
 hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t value, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t value, hipStream_t s);
 

@@ -92,6 +92,7 @@ for name, res, args in [
     ("orc_tile_to_bytes", None, [_P, _P]),
     ("orc_record_checksum", ctypes.c_uint32, [ctypes.c_uint64, ctypes.c_uint32, _P]),
     ("orc_eventlog_record", None, [ctypes.c_uint64, ctypes.c_uint32, _P, ctypes.c_uint32, _P]),
+    ("orc_observe_scores", None, [_P, _P, _SZ, _P, _SZ, _F, _P]),
 ]:
     fn = getattr(lib, name)
     fn.restype = res
@@ -369,3 +370,14 @@ def eventlog_records(tiles, slots, seqs, version: int = 2) -> np.ndarray:
         lib.orc_eventlog_record(int(sq), int(sl), _p(one), version, _p(row))
         out[i] = row
     return out
+
+
+def observe_scores(importance, scores, live, temperature: float, slots=None) -> np.ndarray:
+    """ccos.rs:257-300 on a copy of `importance` (f32 [n_slots]); scores are
+    per slot (slots = arange) unless `slots` is given."""
+    imp = np.ascontiguousarray(importance, np.float32).copy()
+    sc = np.ascontiguousarray(scores, np.float32)
+    sl = np.arange(len(sc), dtype=np.uint32) if slots is None else np.ascontiguousarray(slots, np.uint32)
+    lv = np.ascontiguousarray(live, np.uint8)
+    lib.orc_observe_scores(_p(sl), _p(sc), len(sc), _p(lv), len(imp), temperature, _p(imp))
+    return imp
