@@ -494,6 +494,45 @@ def run_evict(args) -> int:
     return 0
 
 
+def run_ccos(args) -> int:
+    """CCOS control plane over a device arena (ccos.rs): 4 M slots inserted,
+    then one step = observe_scores over the 4 M scores of the arena (H2O
+    importance, ccos.rs:257-300) on the GPU. Per slot the step must read the
+    score (4 B), the state (1 B) and the importance (4 B) and write the
+    importance (4 B): 13 B algorithmic; the two passes read the score and the
+    state twice."""
+    import torch
+
+    import slhav2_amd as s
+
+    n = 1 << 22
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(0x5EED000B)
+    arena = torch.zeros((n, 128), dtype=torch.uint8, device="cuda")
+    tiles = torch.randint(0, 256, (n, 128), dtype=torch.uint8, device="cuda", generator=g)
+    tiles[:, 118:120] = 0  # flags: HOT INT4
+    cache = s.ElasticKvCache(arena, 1 << 62)
+    cache.insert(tiles)
+    del tiles
+    scores = [torch.randn(n, device="cuda", generator=g) * 4 for _ in range(2)]
+    f = s.lib.slha_ccos_observe_scores
+    vp = ctypes.c_void_p
+    a = [(vp(cache._h), vp(sc.data_ptr()), n, ctypes.c_float(0.7), vp(stream.cuda_stream)) for sc in scores]
+    steps, warmup = min(args.steps, 100), min(args.warmup, 10)
+    ms = timed_steps(lambda i: f(*a[i % 2]), steps, warmup, stream)
+    imp = cache._slots()[2]
+    assert abs(float(imp.sum()) - (steps + warmup)) < 1e-2 * (steps + warmup), "importance mass"
+    cache.close()
+    nbytes = n * 13
+    print(json.dumps(line(
+        "CCOS observe_scores slots/s (H2O importance over a 4 M-slot device arena)", n / (ms * 1e-3),
+        "slots/s", steps, warmup, ms, "f32",
+        {"workload": "CCOS observe_scores after scoring the arena (ccos.rs on the GPU)", "slots": n,
+         "temperature": 0.7, "parallelism": "none (1 GPU)"},
+        roofline=hbm_roofline(nbytes, ms, "observe_stats_kernel + observe_apply_kernel", "ccos"))), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -502,7 +541,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos"], default="c2",
                     help="c2 (default) is the headline; c3/c4/c5 measure the other "
                          "BASELINE configs at full size")
     args = ap.parse_args()
@@ -516,7 +555,7 @@ def main() -> int:
         return copy_calibration()
     if args.config != "c2":
         return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode,
-                "evict": run_evict}[args.config](args)
+                "evict": run_evict, "ccos": run_ccos}[args.config](args)
 
     import torch
 

@@ -3018,87 +3018,178 @@ __global__ __launch_bounds__(256) void tile_scatter_kernel(const uint4* __restri
     if (j == 0 && importance) importance[slot] = 0.0f;
 }
 
-// observe_scores (ccos.rs:257-300) over the scores of slots [0, n), in three
-// launches with fixed reduction orders (so repeated calls agree bit for bit):
-//   1. per workgroup: max of the live scores and a non-finite flag;
-//   2. per workgroup: M = max of pass 1, then sum of exp((s - M) / T);
-//   3. every workgroup: L = sum of pass 2 (same order), then, when the
-//      inputs are valid, importance[s] += exp((s - M) / T) * (1 / L).
-// partial holds 2 * kObsBlocks floats; grid = min(blocks needed, kObsBlocks).
-constexpr uint32_t kObsBlocks = 1024;
+// observe_scores (ccos.rs:257-300) over the scores of slots [0, n), in two
+// launches with fixed reduction orders (repeated calls agree bit for bit):
+//   1. per workgroup: the online softmax statistics of its live scores,
+//      (m, l) with l = sum exp((s - m) / T), and a flag (1: a non-finite live
+//      score, 0: live scores, -1: none);
+//   2. every workgroup merges the statistics in the same order into (M, L)
+//      and, when the inputs are valid, adds exp((s - M) / T) * (1 / L) to the
+//      importance of each live slot.
+// L differs from the reference's sequential sum by rounding only (relative
+// error a few f32 ulps). partial holds 3 * kObsBlocks floats.
+constexpr uint32_t kObsBlocks = 1024, kObsUnroll = 4;
 
-__device__ __forceinline__ float block_reduce_f(float x, bool is_max, float* tmp) {
+struct SoftStat {
+    float m, l;
+};
+
+__device__ __forceinline__ SoftStat soft_merge(SoftStat a, SoftStat b, float t) {
+    const float m = fmaxf(a.m, b.m);
+    if (m == -INFINITY) return {m, 0.0f};
+    const float la = a.m == -INFINITY ? 0.0f : a.l * expf((a.m - m) / t);
+    const float lb = b.m == -INFINITY ? 0.0f : b.l * expf((b.m - m) / t);
+    return {m, la + lb};
+}
+
+__device__ __forceinline__ SoftStat block_soft(SoftStat x, float t, float (*tmp)[4]) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-        const float y = __shfl_xor(x, o);
-        x = is_max ? fmaxf(x, y) : x + y;
+        const SoftStat y = {__shfl_xor(x.m, o), __shfl_xor(x.l, o)};
+        x = soft_merge(x, y, t);
     }
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0) tmp[0][threadIdx.x >> 6] = x.m, tmp[1][threadIdx.x >> 6] = x.l;
+    __syncthreads();
+    SoftStat r = {tmp[0][0], tmp[1][0]};
+#pragma unroll
+    for (int w = 1; w < 4; ++w) r = soft_merge(r, {tmp[0][w], tmp[1][w]}, t);
+    return r;
+}
+
+__device__ __forceinline__ float block_max_f(float x, float* tmp) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
     __syncthreads();
     if ((threadIdx.x & 63u) == 0) tmp[threadIdx.x >> 6] = x;
     __syncthreads();
-    return is_max ? fmaxf(fmaxf(tmp[0], tmp[1]), fmaxf(tmp[2], tmp[3])) : (tmp[0] + tmp[1]) + (tmp[2] + tmp[3]);
+    return fmaxf(fmaxf(tmp[0], tmp[1]), fmaxf(tmp[2], tmp[3]));
 }
 
-// Reduces the first `count` entries of v (count <= kObsBlocks) in a fixed order.
-__device__ __forceinline__ float reduce_partials(const float* v, uint32_t count, bool is_max, float* tmp) {
-    float x = is_max ? -INFINITY : 0.0f;
-    for (uint32_t k = threadIdx.x; k < count; k += 256u) x = is_max ? fmaxf(x, v[k]) : x + v[k];
-    return block_reduce_f(x, is_max, tmp);
-}
+// Slot groups: with VEC, group g is the 4 consecutive slots 4g .. 4g + 3
+// (one 16-byte score load, one 4-byte state load; the caller checks the
+// alignment) for g < n / 4, and the last n % 4 slots are a tail taken by
+// thread 0 of workgroup 0; without VEC a group is one slot. Each thread takes
+// kObsUnroll groups a grid-stride apart per iteration, loaded at an index
+// clamped into range with no branch between the loads, then masked.
+template <bool VEC>
+struct ObsGroups {
+    uint64_t full;  // groups loaded whole
+    __device__ explicit ObsGroups(uint64_t n) : full(VEC ? n / 4 : n) {}
+};
 
-__global__ __launch_bounds__(256) void observe_max_kernel(const float* __restrict__ scores,
-                                                          const uint8_t* __restrict__ state, uint64_t n,
-                                                          float* __restrict__ partial) {
-    __shared__ float tmp[4];
-    float m = -INFINITY, bad = 0.0f, live = 0.0f;
-    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
-        if (state[s] == 2) continue;  // COLD
-        const float x = scores[s];
-        live = 1.0f;
-        if (!isfinite(x)) bad = 1.0f;
-        else m = fmaxf(m, x);
+template <bool VEC>
+__device__ __forceinline__ void load_group(const float* scores, const uint8_t* state, uint64_t g,
+                                           float (&x)[4], uint32_t& st) {
+    if constexpr (VEC) {
+        const float4 v = *reinterpret_cast<const float4*>(scores + 4 * g);
+        st = *reinterpret_cast<const uint32_t*>(state + 4 * g);
+        x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+    } else {
+        x[0] = scores[g];
+        st = state[g] | 0x02020200u;  // slots 1..3 of a one-slot group read as COLD
+        x[1] = x[2] = x[3] = 0.0f;
     }
-    m = block_reduce_f(m, true, tmp);
-    bad = block_reduce_f(bad, true, tmp);
-    live = block_reduce_f(live, true, tmp);
+}
+
+__device__ __forceinline__ void soft_add(SoftStat& st, float& flag, float v, float t) {
+    if (!isfinite(v)) {
+        flag = 1.0f;
+        return;
+    }
+    flag = fmaxf(flag, 0.0f);
+    if (v > st.m) {
+        st.l = (st.m == -INFINITY ? 0.0f : st.l * expf((st.m - v) / t)) + 1.0f;
+        st.m = v;
+    } else {
+        st.l += expf((v - st.m) / t);
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void observe_stats_kernel(const float* __restrict__ scores,
+                                                            const uint8_t* __restrict__ state, uint64_t n,
+                                                            float t, float* __restrict__ partial) {
+    __shared__ float tmp[2][4];
+    SoftStat st = {-INFINITY, 0.0f};
+    float flag = -1.0f;
+    const uint64_t full = ObsGroups<VEC>(n).full;
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t g0 = (uint64_t)blockIdx.x * 256u + threadIdx.x; g0 < full; g0 += stride * kObsUnroll) {
+        float x[kObsUnroll][4];
+        uint32_t sb[kObsUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kObsUnroll; ++u) {
+            const uint64_t g = g0 + u * stride;
+            load_group<VEC>(scores, state, g < full ? g : full - 1, x[u], sb[u]);
+            if (g >= full) sb[u] = 0x02020202u;  // past the end: all COLD
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kObsUnroll; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u) soft_add(st, flag, x[u][k], t);
+    }
+    if (VEC && blockIdx.x == 0 && threadIdx.x == 0)
+        for (uint64_t s = 4 * full; s < n; ++s)
+            if (state[s] != 2) soft_add(st, flag, scores[s], t);
+    st = block_soft(st, t, tmp);
+    flag = block_max_f(flag, tmp[0]);
     if (threadIdx.x == 0) {
-        partial[blockIdx.x] = m;
-        // a non-finite live score poisons the max so pass 3 skips the update
-        partial[kObsBlocks + blockIdx.x] = bad != 0.0f ? 1.0f : (live != 0.0f ? 0.0f : -1.0f);
+        partial[blockIdx.x] = st.m;
+        partial[kObsBlocks + blockIdx.x] = st.l;
+        partial[2 * kObsBlocks + blockIdx.x] = flag;
     }
 }
 
-__global__ __launch_bounds__(256) void observe_sum_kernel(const float* __restrict__ scores,
-                                                          const uint8_t* __restrict__ state, uint64_t n,
-                                                          float temperature, float* __restrict__ partial,
-                                                          float* __restrict__ partial_sum) {
-    __shared__ float tmp[4];
-    const float M = reduce_partials(partial, gridDim.x, true, tmp);
-    float acc = 0.0f;
-    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
-        if (state[s] == 2) continue;
-        const float x = scores[s];
-        if (isfinite(x)) acc += expf((x - M) / temperature);
-    }
-    acc = block_reduce_f(acc, false, tmp);
-    if (threadIdx.x == 0) partial_sum[blockIdx.x] = acc;
-}
-
+template <bool VEC>
 __global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restrict__ scores,
                                                             const uint8_t* __restrict__ state, uint64_t n,
-                                                            float temperature, const float* __restrict__ partial,
-                                                            const float* __restrict__ partial_sum,
+                                                            float t, const float* __restrict__ partial,
                                                             float* __restrict__ importance) {
-    __shared__ float tmp[4];
-    const float M = reduce_partials(partial, gridDim.x, true, tmp);
-    const float flag = reduce_partials(partial + kObsBlocks, gridDim.x, true, tmp);  // 1 bad, 0 ok, -1 no live
-    const float L = reduce_partials(partial_sum, gridDim.x, false, tmp);
-    if (flag != 0.0f || !isfinite(L) || !(L > 0.0f)) return;
-    const float inv = 1.0f / L;
-    for (uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x; s < n; s += (uint64_t)gridDim.x * 256u) {
-        if (state[s] == 2) continue;
-        importance[s] += expf((scores[s] - M) / temperature) * inv;
+    __shared__ float tmp[2][4];
+    SoftStat st = {-INFINITY, 0.0f};
+    float flag = -1.0f;
+    for (uint32_t k = threadIdx.x; k < gridDim.x; k += 256u) {
+        st = soft_merge(st, {partial[k], partial[kObsBlocks + k]}, t);
+        flag = fmaxf(flag, partial[2 * kObsBlocks + k]);
     }
+    st = block_soft(st, t, tmp);
+    flag = block_max_f(flag, tmp[0]);
+    if (flag != 0.0f || !isfinite(st.l) || !(st.l > 0.0f)) return;
+    const float M = st.m, inv = 1.0f / st.l;
+    const uint64_t full = ObsGroups<VEC>(n).full;
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t g0 = (uint64_t)blockIdx.x * 256u + threadIdx.x; g0 < full; g0 += stride * kObsUnroll) {
+        float x[kObsUnroll][4], im[kObsUnroll][4];
+        uint32_t sb[kObsUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kObsUnroll; ++u) {
+            const uint64_t g = g0 + u * stride, gc = g < full ? g : full - 1;
+            load_group<VEC>(scores, state, gc, x[u], sb[u]);
+            if constexpr (VEC) {
+                const float4 v = *reinterpret_cast<const float4*>(importance + 4 * gc);
+                im[u][0] = v.x, im[u][1] = v.y, im[u][2] = v.z, im[u][3] = v.w;
+            } else {
+                im[u][0] = importance[gc];
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kObsUnroll; ++u) {
+            const uint64_t g = g0 + u * stride;
+            if (g >= full) continue;
+#pragma unroll
+            for (int k = 0; k < (VEC ? 4 : 1); ++k)
+                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u) im[u][k] += expf((x[u][k] - M) / t) * inv;
+            if constexpr (VEC)
+                *reinterpret_cast<float4*>(importance + 4 * g) = make_float4(im[u][0], im[u][1], im[u][2], im[u][3]);
+            else
+                importance[g] = im[u][0];
+        }
+    }
+    if (VEC && blockIdx.x == 0 && threadIdx.x == 0)
+        for (uint64_t s = ObsGroups<VEC>(n).full * 4; s < n; ++s)
+            if (state[s] != 2) importance[s] += expf((scores[s] - M) / t) * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -3497,13 +3588,21 @@ size_t observe_workspace_floats() { return 3 * (size_t)kObsBlocks; }
 hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint64_t n, float temperature,
                                  float* importance, float* workspace, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    const uint64_t need = (n + 1023) / 1024;
-    const unsigned blocks = (unsigned)(need < kObsBlocks ? need : kObsBlocks);
-    float* partial = workspace;                   // [max | flag] x kObsBlocks
-    float* partial_sum = workspace + 2 * kObsBlocks;
-    observe_max_kernel<<<blocks, 256, 0, s>>>(scores, state, n, partial);
-    observe_sum_kernel<<<blocks, 256, 0, s>>>(scores, state, n, temperature, partial, partial_sum);
-    observe_apply_kernel<<<blocks, 256, 0, s>>>(scores, state, n, temperature, partial, partial_sum, importance);
+    // 16-byte score loads when the three arrays allow them (importance and
+    // state are the cache's own allocations).
+    const bool vec = (reinterpret_cast<uintptr_t>(scores) | reinterpret_cast<uintptr_t>(importance)) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(state) % 4 == 0;
+    const uint64_t groups = vec ? n / 4 : n;
+    const uint64_t need = (groups + 256 * kObsUnroll - 1) / (256 * kObsUnroll);
+    const unsigned blocks = (unsigned)(need == 0 ? 1 : need < kObsBlocks ? need : kObsBlocks);
+    const float t = temperature;
+    if (vec) {
+        observe_stats_kernel<true><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace);
+        observe_apply_kernel<true><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace, importance);
+    } else {
+        observe_stats_kernel<false><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace);
+        observe_apply_kernel<false><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace, importance);
+    }
     return hipGetLastError();
 }
 

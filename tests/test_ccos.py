@@ -219,15 +219,19 @@ def test_score_all_skips_cold_and_insert_keeps_warm(sa, torch):
 
 
 @pytest.mark.gpu
-def test_observe_scores_matches_oracle(sa, torch):
+@pytest.mark.parametrize("n,offset", [(3000, 0), (2999, 0), (3000, 1)])
+def test_observe_scores_matches_oracle(sa, torch, n, offset):
     """GPU importance against the oracle's sequential f32 update, with COLD
-    slots skipped; invalid inputs leave importance unchanged."""
-    print("ccos observe", flush=True)
-    n = 3000
+    slots skipped; invalid inputs leave importance unchanged. (2999: a slot
+    tail past the 4-slot groups; offset 1: scores not 16-byte aligned, the
+    one-slot path.)"""
+    print(f"ccos observe n={n} offset={offset}", flush=True)
     c = sa.ElasticKvCache(arena(torch, 4096), 1 << 60, policy=sa.PAGE_OLDEST_FIRST)
     pool = tiles_of(sa, torch, 1000, seed=12)
-    for k in range(3):
-        c.insert(pool)
+    c.insert(pool[:n - 2000])
+    c.insert(pool)
+    c.insert(pool)
+    assert len(c) == n
     cold = np.random.default_rng(1).choice(n, 400, replace=False)
     for s in cold:
         c.evict(int(s))
@@ -235,17 +239,19 @@ def test_observe_scores_matches_oracle(sa, torch):
     live[cold] = 0
     r = np.random.default_rng(2)
     imp = np.zeros(n, np.float32)
+    buf = torch.empty(n + offset, device="cuda")
     for step in range(4):
         sc = (r.standard_normal(n) * 4).astype(np.float32)
         sc[cold[:5]] = np.nan  # COLD slots never count
-        c.observe_scores(torch.from_numpy(sc).cuda(), 0.7)
+        buf[offset:] = torch.from_numpy(sc).cuda()
+        c.observe_scores(buf[offset:], 0.7)
         imp = o.observe_scores(imp, sc, live, 0.7)
         got = c._slots()[2]
         np.testing.assert_allclose(got, imp, rtol=1e-5, atol=1e-8)
         assert not got[cold].any()
     before = c._slots()[2].copy()
     bad = np.zeros(n, np.float32)
-    bad[int(np.nonzero(live)[0][0])] = np.inf
+    bad[int(np.nonzero(live)[0][-1])] = np.inf
     c.observe_scores(torch.from_numpy(bad).cuda(), 1.0)
     for t in (0.0, -1.0, float("nan"), float("inf")):
         c.observe_scores(torch.zeros(n, device="cuda"), t)
