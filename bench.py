@@ -223,6 +223,14 @@ def hbm_roofline(nbytes: float, ms: float, kernel: str, label: str) -> dict:
             "algorithmic_bytes_per_launch": nbytes, "kernel_ms": ms}
 
 
+def valu_roofline(flops: float, ms: float, kernel: str) -> dict:
+    """f32 VALU work (multiply + add counted as 2 flops) against MI355X's
+    157.3 TFLOP/s f32 peak; traffic is not measured for these kernels."""
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"bound": "valu", "achieved": tf, "peak": 157.3, "unit": "TFLOP/s", "frac": tf / 157.3,
+            "traffic": None, "kernel": kernel, "algorithmic_flops_per_launch": flops, "kernel_ms": ms}
+
+
 def c3_keys(torch, g, rows: int, n_tok: int, outlier_seed: int):
     """bf16 Student-t(4) keys, [rows, n_tok, 128]; per KV head 4 fixed distinct
     outlier channels scaled x20 (rows = seq * 8 + head)."""
@@ -533,6 +541,49 @@ def run_ccos(args) -> int:
     return 0
 
 
+def run_learned(args) -> int:
+    """Learned d > 128 model (learned.rs:257-408, the llama.cpp caller's
+    n_embd_gqa = 1024): a .slhw v2 projection P [128][1024] with RHT
+    (d_pad 1024) loaded through slha_weights_load; one step encodes 32 768
+    bf16 keys (INT4) bit-exactly on the GPU. Also reported: queries prepared/s
+    over 4 096 queries. Per key the encode reads the key (2 KiB) and writes the
+    tile (128 B); P (512 KiB) and Z (1 MiB) stay in L2. The work is f32
+    multiply-adds in the reference's sequential order: h = P k (128 d), the
+    reconstruction (128 d), the sign sketch over d_pad (256 d_pad), i.e.
+    2 * 512 * d flops per key at d = d_pad."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    import slhav2_amd as s
+
+    d, n, nq = 1024, 32768, 4096
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(0x5EED000C)
+    p = (rng.standard_normal((128, d)) / np.sqrt(d)).astype(np.float32)
+    g = torch.Generator(device="cuda").manual_seed(0x5EED000D)
+    keys = torch.randn((1, n, d), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((nq, d), device="cuda", generator=g).to(torch.bfloat16)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = f"{tmp}/bench.slhw"
+        s.save_weights(path, p, seed=0x5EED000E, rht=True)
+        model = s.Model.load(path)
+    out = torch.empty((1, n, 128), dtype=torch.uint8, device="cuda")
+    steps, warmup = min(args.steps, 20), min(args.warmup, 3)
+    ms = timed_steps(lambda i: s.gpu_encode(model, keys, s.CODEC_INT4_SINGLE, out=out), steps, warmup, stream)
+    ms_q = timed_steps(lambda i: s.gpu_prepare_queries(model, q), steps, warmup, stream)
+    model.release()
+    print(json.dumps(line(
+        "learned-model keys encoded/s (d = 1024, RHT, INT4, bit-exact)", n / (ms * 1e-3), "keys/s", steps,
+        warmup, ms, "f32",
+        {"workload": "LearnedModel encode on the GPU (learned.rs:353-408, .slhw v2)", "d": d, "d_pad": 1024,
+         "keys": n, "key_dtype": "bf16", "codec": "int4", "parallelism": "none (1 GPU)"},
+        roofline=valu_roofline(n * 2.0 * 128 * 4 * d, ms, "slha::learned_encode_kernel<0>"),
+        queries={"queries_per_s": nq / (ms_q * 1e-3), "ms_per_launch": ms_q, "queries": nq})), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -541,7 +592,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos", "learned"], default="c2",
                     help="c2 (default) is the headline; c3/c4/c5 measure the other "
                          "BASELINE configs at full size")
     args = ap.parse_args()
@@ -555,7 +606,7 @@ def main() -> int:
         return copy_calibration()
     if args.config != "c2":
         return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode,
-                "evict": run_evict, "ccos": run_ccos}[args.config](args)
+                "evict": run_evict, "ccos": run_ccos, "learned": run_learned}[args.config](args)
 
     import torch
 

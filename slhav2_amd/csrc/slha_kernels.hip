@@ -2312,10 +2312,28 @@ __host__ __device__ constexpr size_t learned_lds_bytes(uint32_t d, uint32_t d_pa
 }
 
 // Sequential f32 dot product sum_i row[i] * v[i], i = 0 .. n-1 (v in LDS).
+// The row (P or Z, read from L2) is loaded kDotBatch float4s at a time, all
+// issued before the batch's sequential adds, so one L2 latency is paid per
+// 64 terms instead of per 4; the sum order is unchanged.
+constexpr uint32_t kDotBatch = 16;
+
 __device__ __forceinline__ float seq_dot(const float* __restrict__ row, const float* v, uint32_t n) {
     float acc = 0.0f;
     uint32_t i = 0;
     if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+        for (; i + 4 * kDotBatch <= n; i += 4 * kDotBatch) {
+            float4 r[kDotBatch];
+#pragma unroll
+            for (uint32_t b = 0; b < kDotBatch; ++b) r[b] = *reinterpret_cast<const float4*>(row + i + 4 * b);
+#pragma unroll
+            for (uint32_t b = 0; b < kDotBatch; ++b) {
+                const uint32_t j = i + 4 * b;
+                acc += r[b].x * v[j];
+                acc += r[b].y * v[j + 1];
+                acc += r[b].z * v[j + 2];
+                acc += r[b].w * v[j + 3];
+            }
+        }
         for (; i + 4 <= n; i += 4) {
             const float4 r = *reinterpret_cast<const float4*>(row + i);
             acc += r.x * v[i];
