@@ -1457,9 +1457,9 @@ __global__ __launch_bounds__(kSegThreads, 2) void topk_segment_kernel(
     const uint32_t n = len - start < kTopkSeg ? len - start : kTopkSeg;
     const uint32_t kk = k < n ? k : n;
     constexpr int PER = kTopkSeg / kSegThreads;
-    // Item j of thread t is score start + j*256 + t; the buffer range ends at
-    // the segment's last score, so the loads past it read zero without a
-    // branch and all 64 are in flight together.
+    // Item j of thread t is score start + j * kSegThreads + t; the buffer
+    // range ends at the segment's last score, so the loads past it read zero
+    // without a branch and all PER are in flight together.
     const float* sc = scores + sbase + (size_t)qh * len + start;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(sc), 0, __builtin_amdgcn_readfirstlane(n * 4u), 0x00020000);
