@@ -2445,6 +2445,154 @@ __global__ __launch_bounds__(256) void learned_encode_kernel(const void* __restr
     }
 }
 
+// Two keys per workgroup (learned_encode_kernel's steps, each key's sums in
+// the same order): threads 0-127 form key 0's latent and 128-255 key 1's;
+// every reconstruction and sign-sketch thread runs both keys' chains side by
+// side on one load of P or Z. Used when both keys' vectors fit in LDS.
+__host__ __device__ constexpr size_t learned_lds_bytes2(uint32_t d, uint32_t d_pad) {
+    return (2 * (size_t)d + 2 * (size_t)d_pad + 256 + 64) * 4;
+}
+
+constexpr uint32_t kDot2Batch = 8;  // float4s per batch with two chains (register budget)
+
+__device__ __forceinline__ void seq_dot2(const float* __restrict__ row, const float* v0, const float* v1,
+                                         uint32_t n, float& a0, float& a1) {
+    float x0 = 0.0f, x1 = 0.0f;
+    uint32_t i = 0;
+    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+        for (; i + 4 * kDot2Batch <= n; i += 4 * kDot2Batch) {
+            float4 r[kDot2Batch];
+#pragma unroll
+            for (uint32_t b = 0; b < kDot2Batch; ++b) r[b] = *reinterpret_cast<const float4*>(row + i + 4 * b);
+#pragma unroll
+            for (uint32_t b = 0; b < kDot2Batch; ++b) {
+                const uint32_t j = i + 4 * b;
+                x0 += r[b].x * v0[j];
+                x1 += r[b].x * v1[j];
+                x0 += r[b].y * v0[j + 1];
+                x1 += r[b].y * v1[j + 1];
+                x0 += r[b].z * v0[j + 2];
+                x1 += r[b].z * v1[j + 2];
+                x0 += r[b].w * v0[j + 3];
+                x1 += r[b].w * v1[j + 3];
+            }
+        }
+    }
+    for (; i < n; ++i) {
+        x0 += row[i] * v0[i];
+        x1 += row[i] * v1[i];
+    }
+    a0 = x0, a1 = x1;
+}
+
+// block_rht over two buffers with one set of workgroup barriers.
+__device__ __forceinline__ void block_rht2(float* b0, float* b1, const float* __restrict__ diag,
+                                           uint32_t d_pad, float inv) {
+    for (uint32_t i = threadIdx.x; i < 2 * d_pad; i += blockDim.x) {
+        float* b = i < d_pad ? b0 : b1;
+        const uint32_t e = i < d_pad ? i : i - d_pad;
+        b[e] *= diag[e];
+    }
+    __syncthreads();
+    const uint32_t half = d_pad / 2;
+    for (uint32_t h = 1; h < d_pad; h <<= 1) {
+        for (uint32_t q2 = threadIdx.x; q2 < 2 * half; q2 += blockDim.x) {
+            float* b = q2 < half ? b0 : b1;
+            const uint32_t q = q2 < half ? q2 : q2 - half;
+            const uint32_t j = ((q & ~(h - 1u)) << 1) | (q & (h - 1u));
+            const float x = b[j], y = b[j + h];
+            b[j] = x + y;
+            b[j + h] = x - y;
+        }
+        __syncthreads();
+    }
+    for (uint32_t i = threadIdx.x; i < 2 * d_pad; i += blockDim.x) {
+        float* b = i < d_pad ? b0 : b1;
+        b[i < d_pad ? i : i - d_pad] *= inv;
+    }
+    __syncthreads();
+}
+
+template <int CODEC>
+__global__ __launch_bounds__(256, (CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped || CODEC == kCodecMixed) ? 3 : 2) void learned_encode2_kernel(const void* __restrict__ keys, int dtype,
+                                                              uint64_t n_keys, uint32_t n_tok,
+                                                              uint32_t n_kv, uint32_t pos0, int warm,
+                                                              LearnedArgs a, float lambda_c,
+                                                              uint4* __restrict__ tiles) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* key0 = lds;
+    float* key1 = key0 + a.d;
+    float* buf0 = key1 + a.d;
+    float* buf1 = buf0 + a.d_pad;
+    float* h0 = buf1 + a.d_pad;
+    float* h1 = h0 + 128;
+    uint32_t* misc0 = reinterpret_cast<uint32_t*>(h1 + 128);  // sign words 0..7, sigma 8
+    uint32_t* misc1 = misc0 + 32;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    for (uint64_t k0 = 2 * (uint64_t)blockIdx.x; k0 < n_keys; k0 += 2 * (uint64_t)gridDim.x) {
+        const bool two = k0 + 1 < n_keys;  // uniform over the workgroup
+        lds_load_vec(keys, dtype, k0, a.d, key0);
+        if (two) lds_load_vec(keys, dtype, k0 + 1, a.d, key1);
+        __syncthreads();
+        if (tid < 128) h0[tid] = seq_dot(a.p + (size_t)tid * a.d, key0, a.d);
+        else if (two) h1[tid - 128] = seq_dot(a.p + (size_t)(tid - 128) * a.d, key1, a.d);
+        __syncthreads();
+        for (uint32_t i = tid; i < a.d; i += blockDim.x) {
+            float r0 = 0.0f, r1 = 0.0f;
+            for (uint32_t k = 0; k < 128; ++k) {
+                const float pk = a.p[(size_t)k * a.d + i];
+                r0 += h0[k] * pk;
+                r1 += h1[k] * pk;
+            }
+            buf0[i] = key0[i] - r0;
+            buf1[i] = key1[i] - r1;
+        }
+        for (uint32_t i = a.d + tid; i < a.d_pad; i += blockDim.x) buf0[i] = buf1[i] = 0.0f;
+        __syncthreads();
+        if ((tid & 63u) == 0 && wave < 2) {  // sigma of key `wave` (learned.rs:392-396)
+            const float* b = wave == 0 ? buf0 : buf1;
+            float acc = 0.0f;
+            for (uint32_t i = 0; i < a.d; ++i) acc += b[i] * b[i];
+            (wave == 0 ? misc0 : misc1)[8] = __float_as_uint(sqrtf(acc / (float)a.d));
+        }
+        __syncthreads();
+        if (a.diag) block_rht2(buf0, buf1, a.diag, a.d_pad, a.rht_inv);
+        {
+            float acc0, acc1;
+            seq_dot2(a.z + (size_t)tid * a.d_pad, buf0, buf1, a.d_pad, acc0, acc1);
+            const uint64_t m0 = __ballot(acc0 < 0.0f), m1 = __ballot(acc1 < 0.0f);
+            if ((tid & 63u) == 0) {
+                misc0[2 * wave] = (uint32_t)m0, misc0[2 * wave + 1] = (uint32_t)(m0 >> 32);
+                misc1[2 * wave] = (uint32_t)m1, misc1[2 * wave + 1] = (uint32_t)(m1 >> 32);
+            }
+        }
+        __syncthreads();
+        if ((tid & 63u) == 0 && (wave == 0 || (wave == 1 && two))) {
+            const uint64_t ki = k0 + wave;
+            const float* h = wave == 0 ? h0 : h1;
+            const uint32_t* misc = wave == 0 ? misc0 : misc1;
+            uint32_t lw[16], gsw[2];
+            float scale;
+            const uint32_t codec_flag = quantize<CODEC>(h, lw, &scale, gsw);
+            const float sigma = __uint_as_float(misc[8]);
+            const float lambda = sigma * lambda_c;
+            const uint32_t row = (uint32_t)(ki / n_tok);
+            const uint32_t pos = pos0 + (uint32_t)(ki - (uint64_t)row * n_tok);
+            const uint32_t flags = codec_flag | (warm ? kFlagWarm : 0u);
+            uint4* out = tiles + ki * 8;
+            out[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            out[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+            out[2] = make_uint4(lw[8], lw[9], lw[10], lw[11]);
+            out[3] = make_uint4(lw[12], lw[13], lw[14], lw[15]);
+            out[4] = make_uint4(misc[0], misc[1], misc[2], misc[3]);
+            out[5] = make_uint4(misc[4], misc[5], misc[6], misc[7]);
+            out[6] = make_uint4(__float_as_uint(scale), __float_as_uint(lambda), misc[8], pos);
+            out[7] = make_uint4(pos, (row % n_kv) | (flags << 16), gsw[0], gsw[1]);
+        }
+        __syncthreads();
+    }
+}
+
 // Query -> (q_coarse [128], q_sign [4]) (slha_prepare_query, lib.rs:420-463:
 // query_coarse, learned.rs:267-273, and sign_bits of the query itself).
 __global__ __launch_bounds__(256) void learned_prepare_kernel(const void* __restrict__ q, int dtype,
@@ -3402,6 +3550,8 @@ LearnedArgs learned_args(const LearnedProjection& lp) {
     return LearnedArgs{lp.p, lp.z, lp.diag, lp.d, lp.d_pad, lp.rht_inv};
 }
 unsigned learned_grid(uint64_t n) { return (unsigned)std::min<uint64_t>(n, 1u << 20); }
+constexpr size_t kLdsMaxBytes = 160 * 1024;  // LDS per workgroup on gfx950
+
 // Dynamic LDS above the default 64 KiB needs the kernel's opt-in.
 template <typename K>
 hipError_t allow_lds(K kernel, size_t bytes) {
@@ -3419,8 +3569,18 @@ hipError_t launch_learned_encode(const void* keys, int dtype, uint64_t n_keys, u
     const size_t lds = learned_lds_bytes(lp.d, lp.d_pad);
     uint4* out = static_cast<uint4*>(tiles);
     const LearnedArgs a = learned_args(lp);
+    // Two keys per workgroup when both keys' vectors fit in LDS.
+    const size_t lds2 = learned_lds_bytes2(lp.d, lp.d_pad);
+    const bool pair = lds2 <= kLdsMaxBytes;
 #define SLHA_LEARNED_ENC(C)                                                                        \
     {                                                                                              \
+        if (pair) {                                                                                \
+            const hipError_t e = allow_lds(learned_encode2_kernel<C>, lds2);                        \
+            if (e != hipSuccess) return e;                                                         \
+            learned_encode2_kernel<C><<<learned_grid((n_keys + 1) / 2), 256, lds2, s>>>(            \
+                keys, dtype, n_keys, n_tok, n_kv, pos0, warm, a, lambda_c, out);                   \
+            break;                                                                                 \
+        }                                                                                          \
         const hipError_t e = allow_lds(learned_encode_kernel<C>, lds);                              \
         if (e != hipSuccess) return e;                                                             \
         learned_encode_kernel<C><<<learned_grid(n_keys), 256, lds, s>>>(keys, dtype, n_keys, n_tok, \
