@@ -2618,6 +2618,52 @@ __global__ __launch_bounds__(256) void learned_prepare_kernel(const void* __rest
     }
 }
 
+// Two queries per workgroup (learned_prepare_kernel's steps, each sum in its
+// order): threads 0-127 form query 0's q_coarse and 128-255 query 1's; the
+// sketch threads run both chains on one load of Z.
+__global__ __launch_bounds__(256) void learned_prepare2_kernel(const void* __restrict__ q, int dtype,
+                                                               uint64_t n_q, LearnedArgs a,
+                                                               float* __restrict__ qc,
+                                                               uint64_t* __restrict__ qs) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* vec0 = lds;
+    float* vec1 = vec0 + a.d;
+    float* buf0 = vec1 + a.d;
+    float* buf1 = buf0 + a.d_pad;
+    uint32_t* words = reinterpret_cast<uint32_t*>(buf1 + a.d_pad);  // [2][8]
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    for (uint64_t q0 = 2 * (uint64_t)blockIdx.x; q0 < n_q; q0 += 2 * (uint64_t)gridDim.x) {
+        const bool two = q0 + 1 < n_q;  // uniform over the workgroup
+        lds_load_vec(q, dtype, q0, a.d, vec0);
+        if (two) lds_load_vec(q, dtype, q0 + 1, a.d, vec1);
+        __syncthreads();
+        for (uint32_t i = tid; i < a.d_pad; i += blockDim.x) {
+            buf0[i] = i < a.d ? vec0[i] : 0.0f;
+            buf1[i] = i < a.d && two ? vec1[i] : 0.0f;
+        }
+        if (tid < 128) qc[q0 * 128 + tid] = seq_dot(a.p + (size_t)tid * a.d, vec0, a.d);
+        else if (two) qc[(q0 + 1) * 128 + tid - 128] = seq_dot(a.p + (size_t)(tid - 128) * a.d, vec1, a.d);
+        __syncthreads();
+        if (a.diag) block_rht2(buf0, buf1, a.diag, a.d_pad, a.rht_inv);
+        {
+            float acc0, acc1;
+            seq_dot2(a.z + (size_t)tid * a.d_pad, buf0, buf1, a.d_pad, acc0, acc1);
+            const uint64_t m0 = __ballot(acc0 < 0.0f), m1 = __ballot(acc1 < 0.0f);
+            if ((tid & 63u) == 0) {
+                words[2 * wave] = (uint32_t)m0, words[2 * wave + 1] = (uint32_t)(m0 >> 32);
+                words[8 + 2 * wave] = (uint32_t)m1, words[8 + 2 * wave + 1] = (uint32_t)(m1 >> 32);
+            }
+        }
+        __syncthreads();
+        if (tid < (two ? 8u : 4u)) {
+            const uint32_t w = tid & 3u, which = tid >> 2;
+            qs[(q0 + which) * 4 + w] =
+                (uint64_t)words[8 * which + 2 * w] | ((uint64_t)words[8 * which + 2 * w + 1] << 32);
+        }
+        __syncthreads();
+    }
+}
+
 // Tile -> key estimate [d]: reconstruct(dequant_latent) (slha_decode_latent,
 // lib.rs:763-822), plus with_residual the sign-sketch term of
 // reconstruct_from_tile (learned.rs:288-320), omitted for RHT models.
@@ -3604,6 +3650,14 @@ hipError_t launch_learned_encode(const void* keys, int dtype, uint64_t n_keys, u
 hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const LearnedProjection& lp,
                                   float* qc, uint64_t* qs, hipStream_t s) {
     if (n_q == 0) return hipSuccess;
+    const size_t lds2 = learned_lds_bytes2(lp.d, lp.d_pad);
+    if (lds2 <= kLdsMaxBytes) {  // two queries per workgroup
+        const hipError_t e = allow_lds(learned_prepare2_kernel, lds2);
+        if (e != hipSuccess) return e;
+        learned_prepare2_kernel<<<learned_grid((n_q + 1) / 2), 256, lds2, s>>>(q, dtype, n_q, learned_args(lp),
+                                                                                qc, qs);
+        return hipGetLastError();
+    }
     const size_t lds = learned_lds_bytes(lp.d, lp.d_pad);
     const hipError_t e = allow_lds(learned_prepare_kernel, lds);
     if (e != hipSuccess) return e;
