@@ -573,6 +573,11 @@ def run_learned(args) -> int:
     steps, warmup = min(args.steps, 20), min(args.warmup, 3)
     ms = timed_steps(lambda i: s.gpu_encode(model, keys, s.CODEC_INT4_SINGLE, out=out), steps, warmup, stream)
     ms_q = timed_steps(lambda i: s.gpu_prepare_queries(model, q), steps, warmup, stream)
+    dec = torch.empty((n, d), dtype=torch.float32, device="cuda")
+    f_dec = s.lib.slha_gpu_decode
+    dec_args = (ctypes.c_void_p(model.handle), ctypes.c_void_p(out.data_ptr()), n, 1, ctypes.c_void_p(dec.data_ptr()),
+                ctypes.c_void_p(stream.cuda_stream))
+    ms_d = timed_steps(lambda i: f_dec(*dec_args), steps, warmup, stream)
     model.release()
     print(json.dumps(line(
         "learned-model keys encoded/s (d = 1024, RHT, INT4, bit-exact)", n / (ms * 1e-3), "keys/s", steps,
@@ -580,7 +585,9 @@ def run_learned(args) -> int:
         {"workload": "LearnedModel encode on the GPU (learned.rs:353-408, .slhw v2)", "d": d, "d_pad": 1024,
          "keys": n, "key_dtype": "bf16", "codec": "int4", "parallelism": "none (1 GPU)"},
         roofline=valu_roofline(n * 2.0 * 128 * 4 * d, ms, "slha::learned_encode2_kernel<0>"),
-        queries={"queries_per_s": nq / (ms_q * 1e-3), "ms_per_launch": ms_q, "queries": nq})), flush=True)
+        queries={"queries_per_s": nq / (ms_q * 1e-3), "ms_per_launch": ms_q, "queries": nq},
+        decode={"tiles_per_s": n / (ms_d * 1e-3), "ms_per_launch": ms_d, "tiles": n, "with_residual": True})),
+        flush=True)
     return 0
 
 

@@ -2674,31 +2674,63 @@ __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __rest
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float* h = lds;
     uint32_t* misc = reinterpret_cast<uint32_t*>(h + 128);  // residual words 0..7, sigma 8
+    __shared__ float cb[16];
     const uint32_t tid = threadIdx.x;
     const bool resid = with_residual && !a.diag;
+    stage_codebook(cb);
+    __syncthreads();
     for (uint64_t ti = blockIdx.x; ti < n; ti += gridDim.x) {
-        if (tid == 0) {
+        if (tid < 8) {  // thread g dequantises dims [16g, 16g + 16), operation for operation
             uint32_t w[32];
             load_tile(tiles + ti * 8, w);
-            float k[kDC];
-            dequant_exact(w, w + 30, __uint_as_float(w[24]), w[29] >> 16, k);
-            for (int d = 0; d < kDC; ++d) h[d] = k[d];
-            for (int j = 0; j < 8; ++j) misc[j] = w[16 + j];
-            misc[8] = w[26];
+            float k[16];
+            switch (codec_class(w[29] >> 16)) {
+                case kClsInt4: decode_group_exact<kClsInt4>(w, (int)tid, cb, k); break;
+                case kClsNF4: decode_group_exact<kClsNF4>(w, (int)tid, cb, k); break;
+                case kClsTQ3: decode_group_exact<kClsTQ3>(w, (int)tid, cb, k); break;
+                case kClsMixed: decode_group_exact<kClsMixed>(w, (int)tid, cb, k); break;
+                default: decode_group_exact<kClsMix3>(w, (int)tid, cb, k); break;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) h[16 * tid + j] = k[j];
+            if (tid == 0) {
+                for (int j = 0; j < 8; ++j) misc[j] = w[16 + j];
+                misc[8] = w[26];
+            }
         }
         __syncthreads();
         // (sigma * sqrt(pi/2)) / 256, learned.rs:303
         const float sc = __uint_as_float(misc[8]) * sqrt_half_pi / 256.0f;
-        for (uint32_t i = tid; i < a.d; i += blockDim.x) {
-            float r = 0.0f;
-            for (uint32_t k = 0; k < 128; ++k) r += h[k] * a.p[(size_t)k * a.d + i];
+        // kDecU outputs per thread side by side (each its own sequential
+        // sum), so every step has kDecU independent loads and adds; lanes
+        // past d compute a clamped copy and do not store.
+        constexpr uint32_t kDecU = 4;
+        for (uint32_t i0 = tid; i0 < a.d; i0 += blockDim.x * kDecU) {
+            uint32_t ii[kDecU];
+            float r[kDecU];
+#pragma unroll
+            for (uint32_t u = 0; u < kDecU; ++u) {
+                const uint32_t i = i0 + u * blockDim.x;
+                ii[u] = i < a.d ? i : a.d - 1u;
+                r[u] = 0.0f;
+            }
+            for (uint32_t k = 0; k < 128; ++k) {
+                const float hk = h[k];
+                const float* pk = a.p + (size_t)k * a.d;
+#pragma unroll
+                for (uint32_t u = 0; u < kDecU; ++u) r[u] += hk * pk[ii[u]];
+            }
             if (resid) {
                 for (uint32_t s = 0; s < kDS; ++s) {
                     const float sgn = ((misc[s >> 5] >> (s & 31u)) & 1u) ? -1.0f : 1.0f;
-                    r += sgn * sc * a.z[(size_t)s * a.d_pad + i];
+                    const float* zs = a.z + (size_t)s * a.d_pad;
+#pragma unroll
+                    for (uint32_t u = 0; u < kDecU; ++u) r[u] += sgn * sc * zs[ii[u]];
                 }
             }
-            out[ti * a.d + i] = r;
+#pragma unroll
+            for (uint32_t u = 0; u < kDecU; ++u)
+                if (i0 + u * blockDim.x < a.d) out[ti * a.d + i0 + u * blockDim.x] = r[u];
         }
         __syncthreads();
     }
