@@ -347,36 +347,40 @@ def run_decode(args) -> int:
     import slhav2_amd as s
 
     n_sets, d_v = 4, 128
+    group = args.group
+    n_q = N_KV * group
     stream = torch.cuda.current_stream()
     g = torch.Generator(device="cuda").manual_seed(0x5EED0007)
     model = s.Model(seed=0x5EED0002, rht=False, residual_mode=s.RESIDUAL_R)
-    queries = torch.randn((N_Q, D), device="cuda", generator=g).to(torch.bfloat16)
+    queries = torch.randn((n_q, D), device="cuda", generator=g).to(torch.bfloat16)
     qc, qs = s.gpu_prepare_queries(model, queries)
     sets = []
     for _ in range(n_sets):
         keys = torch.randn((N_KV, N_TOK, D), device="cuda", generator=g).to(torch.bfloat16)
         vals = torch.randn((N_KV, N_TOK, d_v), device="cuda", generator=g).to(torch.bfloat16)
         sets.append((s.gpu_encode(model, keys, s.CODEC_INT4_SINGLE, n_kv_heads=N_KV), vals))
-    out = torch.empty((N_Q, d_v), dtype=torch.float32, device="cuda")
+    out = torch.empty((n_q, d_v), dtype=torch.float32, device="cuda")
     scale = 1.0 / np.sqrt(float(D))
     f = s.lib.slha_gpu_decode_attention
     vp = ctypes.c_void_p
     args_k = [(vp(t.data_ptr()), vp(v.data_ptr()), s.DTYPE_BF16, N_KV, N_TOK, d_v, vp(qc.data_ptr()),
-               vp(qs.data_ptr()), GROUP, ctypes.c_float(scale), vp(out.data_ptr()),
+               vp(qs.data_ptr()), group, ctypes.c_float(scale), vp(out.data_ptr()),
                vp(stream.cuda_stream)) for t, v in sets]
     steps, warmup = min(args.steps, 100), min(args.warmup, 10)
     ms = timed_steps(lambda i: f(*args_k[i % n_sets]), steps, warmup, stream)
     model.release()
-    nbytes = N_KV * N_TOK * (TILE_BYTES + d_v * 2) + N_Q * (D * 4 + 32) + N_Q * d_v * 4
+    nbytes = N_KV * N_TOK * (TILE_BYTES + d_v * 2) + n_q * (D * 4 + 32) + n_q * d_v * 4
     print(json.dumps(line(
-        "decode attention steps/s over compressed keys (32k ctx, 32 heads)", 1.0 / (ms * 1e-3),
+        f"decode attention steps/s over compressed keys (32k ctx, {n_q} heads)", 1.0 / (ms * 1e-3),
         "steps/s", steps, warmup, ms, "f32",
         {"workload": "decode attention at the C2 shape (benchmark_decode.rs on the GPU)",
-         "kv_heads": N_KV, "tokens_per_head": N_TOK, "query_heads": N_Q, "group": GROUP,
+         "kv_heads": N_KV, "tokens_per_head": N_TOK, "query_heads": n_q, "group": group,
          "d_v": d_v, "v_dtype": "bf16", "codec": "int4", "cold_cache_rotation_sets": n_sets,
          "parallelism": "none (1 GPU)"},
-        roofline=hbm_roofline(nbytes, ms, "attn_fused_kernel + attn_combine_kernel", "decode"),
-        tokens_attended_per_s=N_Q * N_TOK / (ms * 1e-3))), flush=True)
+        roofline=hbm_roofline(nbytes, ms, "attn_fused_kernel + attn_combine_kernel" if group <= 4 else
+                              "score_rows_fast_kernel + attn_partial_kernel + attn_combine_kernel",
+                              "decode" if group == GROUP else f"decode_g{group}"),
+        tokens_attended_per_s=n_q * N_TOK / (ms * 1e-3))), flush=True)
     return 0
 
 
@@ -597,6 +601,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--group", type=int, default=GROUP,
+                    help="GQA group of --config decode (default 4, the C2 shape; 1..16)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
     ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos", "learned"], default="c2",

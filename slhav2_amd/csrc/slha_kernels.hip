@@ -2752,7 +2752,11 @@ __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __rest
 // logits -inf) do not arise here.
 constexpr uint32_t kAttnSeg = 256;  // tokens per partial block (one per thread in phase 1)
 constexpr uint32_t kAttnMaxGroup = 16;
-constexpr uint32_t kAttnFusedMaxGroup = 4;  // groups scored inside attn_fused_kernel
+// Groups scored inside attn_fused_kernel: up to 4 at any d_v, up to 8 while
+// a wave's weights and o_w ([G][64 + d_v] floats) fit its 8 KiB tile region.
+__host__ __device__ constexpr bool attn_fused_ok(uint32_t group, uint32_t d_v) {
+    return group <= 4 || (group <= 8 && d_v <= 128);
+}
 
 __host__ __device__ constexpr size_t attn_partial_floats(uint32_t d_v) { return (size_t)d_v + 4; }
 
@@ -2902,7 +2906,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     }
 }
 
-// Fused segment kernel for group <= kAttnFusedMaxGroup, grid (n_seg, n_rows), 256 threads.
+// Fused segment kernel for attn_fused_ok(group, d_v), G = 4 or 8 (queries
+// staged per row), grid (n_seg, n_rows), 256 threads.
 // Wave w scores tokens t0 + 64 w .. +63 exactly as score_rows_fast_kernel<4>
 // scores them (same tile DMA, query staging and MFMA paths) and runs a
 // flash-decoding step over its own 64 tokens: wave max m_w, weights
@@ -2912,14 +2917,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
 // read its tiles back, its 8 KiB tile region holds its weights [G][64] and
 // then its o_w [G][DV], so the block needs about 37 KiB of LDS and, at <= 128
 // VGPRs, four blocks share a CU: the decode grid (128 x 8) is resident at once.
-template <int VDT, int DV>
-__global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restrict__ tiles,
+template <int VDT, int DV, int G>
+__global__ __launch_bounds__(256, G <= 4 ? 4 : 3) void attn_fused_kernel(const uint4* __restrict__ tiles,
                                                             uint32_t n_tok, uint32_t group,
                                                             const float* __restrict__ qc,
                                                             const uint32_t* __restrict__ qs,
                                                             const void* __restrict__ vals,
                                                             float scale, float* __restrict__ part) {
-    constexpr int G = (int)kAttnFusedMaxGroup;
     constexpr int VEC = VDT == kDtypeBF16 ? 8 : 4;  // V elements per 16-byte load
     constexpr int LPT = DV / VEC, TPW = 64 / LPT;   // lanes per token, tokens per wave step
     constexpr uint32_t kSteps = 64 / TPW;
@@ -2927,7 +2931,7 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
     static_assert(G * (64 + DV) * 4 <= 512 * 16, "weights and o_w fit the tile region");
     __shared__ float cb[16];
     __shared__ uint4 tile_lds[4][512];
-    __shared__ __attribute__((aligned(16))) float qstatic[staging_bytes(4) / 4];
+    __shared__ __attribute__((aligned(16))) float qstatic[staging_bytes(G) / 4];
     __shared__ float wst[4][G][3];  // per wave: m_w, l_w, NaN seen
     const uint32_t seg = blockIdx.x, row = blockIdx.y, n_seg = gridDim.x;
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
@@ -2938,12 +2942,12 @@ __global__ __launch_bounds__(256, 4) void attn_fused_kernel(const uint4* __restr
     float* ew = reinterpret_cast<float*>(tile_lds[wave]);  // [G][64] after the readback
     float* ow = ew + G * 64;                               // [G][DV]
     {
-        const StagedQueries sq = carve_staging(qstatic, 4);
-        QueryRegs<4> qr;
-        stage_issue<4>(qc, qrow0, group, qr);
+        const StagedQueries sq = carve_staging(qstatic, G);
+        QueryRegs<G> qr;
+        stage_issue<G>(qc, qrow0, group, qr);
         fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
         stage_codebook(cb);
-        stage_commit<4>(qr, group, sq);
+        stage_commit<G>(qr, group, sq);
         lds_barrier();
         uint32_t w[32];
         fetch_tiles_readback(tile_lds[wave], w);
@@ -3723,7 +3727,7 @@ hipError_t attn_partial_dv(dim3 grid, const float* scores, const void* vals, uin
 template <int VDT>
 hipError_t attn_partial_g(dim3 grid, const float* scores, const void* vals, uint32_t n_tok,
                           uint32_t group, uint32_t d_v, float scale, float* part, hipStream_t s) {
-    // group <= kAttnFusedMaxGroup runs attn_fused_kernel instead
+    // attn_fused_ok(group, d_v) runs attn_fused_kernel instead
     if (group <= 8) return attn_partial_dv<VDT, 8>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
     return attn_partial_dv<VDT, 16>(grid, scores, vals, n_tok, group, d_v, scale, part, s);
 }
@@ -3740,7 +3744,7 @@ size_t decode_attention_workspace_bytes(uint32_t n_rows, uint32_t n_tok, uint32_
                                         uint32_t d_v) {
     const size_t n_seg = (n_tok + kAttnSeg - 1) / kAttnSeg;
     const size_t part = (size_t)n_rows * n_seg * group * attn_partial_floats(d_v) * 4;
-    if (group <= kAttnFusedMaxGroup) return part;
+    if (attn_fused_ok(group, d_v)) return part;
     const size_t scores = (size_t)n_rows * group * n_tok * 4;
     const size_t wide = score_rows_workspace_bytes(n_rows, group, false, false);
     return ((part + 255) & ~(size_t)255) + ((scores + 255) & ~(size_t)255) + wide;
@@ -3764,21 +3768,25 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
     const uint4* tp = static_cast<const uint4*>(tiles);
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
     hipError_t e = hipSuccess;
-    if (group <= kAttnFusedMaxGroup) {  // scores stay in LDS
+    if (attn_fused_ok(group, d_v)) {  // scores stay in LDS
         const dim3 grid(n_seg, n_rows);
 #define SLHA_FUSED(VDT, DV)                                                                         \
-    attn_fused_kernel<VDT, DV><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part)
+    (group <= 4 ? attn_fused_kernel<VDT, DV, 4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part) \
+                : attn_fused_kernel<VDT, DV, 8><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part))
+#define SLHA_FUSED4(VDT, DV)                                                                        \
+    attn_fused_kernel<VDT, DV, 4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, vals, scale, part)
         switch ((v_dtype == kDtypeBF16 ? 1000 : 0) + (int)d_v) {
             case 32: SLHA_FUSED(kDtypeF32, 32); break;
             case 64: SLHA_FUSED(kDtypeF32, 64); break;
             case 128: SLHA_FUSED(kDtypeF32, 128); break;
-            case 256: SLHA_FUSED(kDtypeF32, 256); break;
+            case 256: SLHA_FUSED4(kDtypeF32, 256); break;
             case 1032: SLHA_FUSED(kDtypeBF16, 32); break;
             case 1064: SLHA_FUSED(kDtypeBF16, 64); break;
             case 1128: SLHA_FUSED(kDtypeBF16, 128); break;
-            case 1256: SLHA_FUSED(kDtypeBF16, 256); break;
+            case 1256: SLHA_FUSED4(kDtypeBF16, 256); break;
             default: return hipErrorInvalidValue;
         }
+#undef SLHA_FUSED4
 #undef SLHA_FUSED
         e = hipGetLastError();
         if (e != hipSuccess) return e;

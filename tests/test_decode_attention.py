@@ -86,6 +86,9 @@ def _setup(s, torch, n_rows, n_tok, group, seed, codec=0):
     (2, 300, 8, 32, "f32"),
     (1, 700, 16, 256, "f32"),
     (1, 5, 2, 128, "f32"),
+    (2, 2000, 8, 128, "bf16"),
+    (1, 777, 6, 64, "f32"),
+    (1, 300, 16, 128, "bf16"),
 ])
 def test_gpu_decode_attention(s, torch, n_rows, n_tok, group, d_v, vdt):
     print(f"decode attention rows={n_rows} tok={n_tok} group={group} d_v={d_v} {vdt}", flush=True)
