@@ -69,7 +69,8 @@ int32_t slha_ccos_attach_event_log(SlhaCcos* c, SlhaEventLog* log, int32_t durab
 /* insert (ccos.rs:213-247) of n device tiles, in order: each takes the last
  * recycled slot (free-list pop) or the next new one; its state follows its
  * FLAG_WARM; importance 0; a new seq. slots_out (host, n) receives the slots.
- * SLHA_ERR_DIMENSION when the arena is full. */
+ * SLHA_ERR_DIMENSION when the arena is full. tiles_dev must not overlap the
+ * arena's recycled slots (the copy into them is one parallel scatter). */
 int32_t slha_ccos_insert(SlhaCcos* c, const SciRustSlhaTile* tiles_dev, size_t n, uint32_t* slots_out,
                          void* stream);
 

@@ -78,7 +78,9 @@ int32_t slha_eventlog_read(SlhaEventLog* log, uint64_t first, size_t n, uint8_t*
 int32_t slha_eventlog_find_seq(SlhaEventLog* log, uint64_t seq, uint64_t* index_out, int32_t* found);
 int32_t slha_eventlog_find_slot(SlhaEventLog* log, uint32_t slot, uint64_t* index_out, int32_t* found);
 
-/* Closes the file and releases the handle. */
+/* Closes the file and releases the handle. Calls on one handle are
+ * serialised by the library, but none may still be starting on it when it is
+ * closed, nor start after. */
 int32_t slha_eventlog_close(SlhaEventLog* log);
 
 /* Device side. ElasticKvCache::evict (ccos.rs:404-438) appends
