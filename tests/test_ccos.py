@@ -418,3 +418,25 @@ def test_evict_snapshots_to_event_log_then_rehydrates_identically(sa, torch, tmp
     d.insert(tiles_of(sa, torch, 3, seed=2))
     d.enforce_budget()
     assert d.log_errors() == 0 and d.rehydrate(0) is None
+
+
+@pytest.mark.gpu
+def test_edge_cases_match_the_reference_contract(sa, torch):
+    """A full arena rejects the insert before any change; evict of a COLD
+    slot, page_out of a WARM slot and drop_correction on a tile without a
+    correction plane change nothing (ccos.rs:369-438)."""
+    c = sa.ElasticKvCache(arena(torch, 4), 1 << 60)
+    t = tiles_of(sa, torch, 5, seed=21)
+    c.insert(t[:4])
+    with pytest.raises(sa.SlhaError) as e:
+        c.insert(t[4:5])
+    assert e.value.code == sa.ERR_DIMENSION and len(c) == 4
+    assert c.evict(1) and not c.evict(1)
+    assert c.live_bytes() == 3 * HOT
+    c.page_out(0)
+    before = c.arena[0].cpu().numpy().tobytes()
+    c.page_out(0)
+    assert c.state(0) == sa.WARM and c.arena[0].cpu().numpy().tobytes() == before
+    assert not c.drop_correction(2)  # INT4: no plane
+    assert c.live_bytes() == 2 * HOT + WARM
+    assert c.insert(t[4:5]) == [1]  # the COLD slot is recycled
