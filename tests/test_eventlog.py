@@ -395,3 +395,19 @@ def test_gpu_evict_log_rehydrate_end_to_end(sa, torch, tmp_path):
     out = fresh.cpu().numpy()
     for s, d in zip([3, 77, 500, 12], [7, 0, 5, 2]):
         assert out[d].tobytes() == before[s].tobytes()
+
+
+def test_empty_log_reads_and_lookups(sa, tmp_path):
+    """A log holding only its header: len 0, read_all empty, lookups find
+    nothing, and it reopens in every mode."""
+    p = tmp_path / "empty"
+    with sa.EventLog.create(p) as log:
+        assert len(log) == 0 and log.version == 2
+        assert len(log.read_all()) == 0
+        assert log.fetch_by_seq(0) is None and log.fetch_last_for_slot(0) is None
+        log.sync()
+    for mode in (sa.EVENTLOG_OPEN_STRICT, sa.EVENTLOG_OPEN_RECOVER, sa.EVENTLOG_OPEN_READ_ONLY):
+        with sa.EventLog.open(p, mode) as log:
+            assert len(log) == 0
+            log.sync()
+    assert p.read_bytes() == struct.pack("<IIII", 0x534C4C47, 2, 128, 0)
