@@ -51,6 +51,66 @@ def test_gaussian_moments_and_determinism():
     assert np.array_equal(g[:100], o.Rng(5).gaussian(100))
 
 
+def _box_muller_f64(u1, u2, variant="ref"):
+    """rng.rs:39-44 in float64 from the pinned next_unit draws:
+    sqrt(-2 ln max(u1, 1e-7)) * cos(2 pi u2). The variants plant the plausible
+    slips (sin for cos, u1 and u2 swapped) to show the check rejects them."""
+    a = np.maximum(u1.astype(np.float64), 1e-7)
+    b = u2.astype(np.float64)
+    if variant == "swap_u":
+        a, b = np.maximum(b, 1e-7), a
+    trig = np.sin if variant == "sin" else np.cos
+    return np.sqrt(-2.0 * np.log(a)) * trig(2.0 * np.pi * b)
+
+
+def _box_muller_close(got, want):
+    # f32 evaluation error: ln, sqrt and the f32 product 2*pi*u2 (the angle is
+    # off by at most ~6e-7 rad, so the cosine by ~6e-7 absolute) give
+    # |got - want| <= r * 1.5e-6 + 4 ulp(|want|). r = sqrt(-2 ln u1) <= 5.7.
+    r = np.sqrt(-2.0 * np.log(1e-7))
+    tol = r * 1.5e-6 + 4 * np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - want) <= tol
+
+
+def test_gaussian_is_box_muller_closed_form():
+    # rng.rs:39-44: u1 = next_unit().max(1e-7), u2 = next_unit(),
+    # r = sqrt(-2 ln u1), g = r cos(2 pi u2). The uniform draws are pinned by
+    # test_next_unit_is_top_24_bits, so the two-draw pairing, the max, and the
+    # trigonometric branch are pinned here against float64.
+    for seed in (0, 5, 2**63 + 11):
+        n = 50000
+        g = o.Rng(seed).gaussian(n)
+        r = o.Rng(seed)
+        u = np.array([r.next_unit() for _ in range(2 * n)], np.float32)
+        u1, u2 = u[0::2], u[1::2]
+        assert _box_muller_close(g, _box_muller_f64(u1, u2)).all()
+        # A planted sin/cos or u1/u2 swap fails on most draws.
+        for bad in ("sin", "swap_u"):
+            assert (~_box_muller_close(g, _box_muller_f64(u1, u2, bad))).mean() > 0.9
+    # u1 = 0 must take the 1e-7 floor. A seed whose first draw is 0 comes from
+    # inverting the SplitMix64 finaliser (rng.rs:22-28) on an output whose top
+    # 24 bits are zero.
+    m64 = 2**64 - 1
+
+    def unshift(x, s):
+        y = x
+        for _ in range(64 // s + 1):
+            y = x ^ (y >> s)
+        return y & m64
+
+    z = 0x0000001234567890
+    z = unshift(z, 31)
+    z = unshift((z * pow(0x94D049BB133111EB, -1, 2**64)) & m64, 27)
+    z = unshift((z * pow(0xBF58476D1CE4E5B9, -1, 2**64)) & m64, 30)
+    seed = ((z - GOLDEN) & m64) ^ GOLDEN
+    r = o.Rng(seed)
+    assert r.next_unit() == 0.0
+    u2 = np.float32(r.next_unit())
+    g = o.Rng(seed).gaussian(1)
+    want = np.sqrt(-2.0 * np.log(1e-7)) * np.cos(2.0 * np.pi * np.float64(u2))
+    assert abs(float(g[0]) - want) <= 1e-5 and abs(want) > 0.1
+
+
 # --- KATs -----------------------------------------------------------------
 
 def test_basic_usage_known_answer():
