@@ -2247,13 +2247,24 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint4* __restrict__
     }
 }
 
-// CCOS ladder (ccos.rs:369-397) on device tiles.
+// CCOS ladder (ccos.rs:369-438) on device tiles: op 0 page_out, op 1
+// drop_correction, op 2 evict (the tile stays, its state becomes COLD). The
+// slots are slots[0, n), or the one slot `slot0` when slots is NULL. With a
+// state array (0 HOT, 1 WARM, 2 COLD), page_out and evict also write the
+// slot's new state.
 __global__ __launch_bounds__(256) void ccos_apply_kernel(uint4* __restrict__ tiles,
+                                                         uint8_t* __restrict__ state,
                                                          const uint32_t* __restrict__ slots,
-                                                         uint64_t n, int op) {
+                                                         uint32_t slot0, uint64_t n, int op) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    uint4* t = tiles + (size_t)slots[i] * 8;
+    const uint32_t slot = slots ? slots[i] : slot0;
+    if (op == 2) {
+        if (state) state[slot] = 2;
+        return;
+    }
+    if (op == 0 && state) state[slot] = 1;
+    uint4* t = tiles + (size_t)slot * 8;
     uint4 m0 = t[6], m1 = t[7];
     uint32_t flags = m1.y >> 16;
     if (op == 0) {  // page_out: residual := 0, lambda := 0, |WARM
@@ -2750,6 +2761,12 @@ __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __rest
 // output; scores of valid tiles against prepared (finite) queries are
 // finite, so the other degenerate cases of softmax_into (+inf logits, all
 // logits -inf) do not arise here.
+// softmax_into forms its logits in f64, where a finite f32 score times a
+// finite scale never overflows. In f32 score * scale can, so the kernels work
+// on t = score * sign(scale) and weigh each token with
+// exp((t - max t) * |scale|): the same weights, and a difference that
+// overflows only pushes a weight to 0, as it is in f64. Partial maxima are
+// kept in t, and the combine scales their differences by |scale| the same way.
 constexpr uint32_t kAttnSeg = 256;  // tokens per partial block (one per thread in phase 1)
 constexpr uint32_t kAttnMaxGroup = 16;
 // Groups scored inside attn_fused_kernel: up to 4 at any d_v, up to 8 while
@@ -2829,7 +2846,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     uint4 x[kDepth];
 #pragma unroll
     for (uint32_t u = 0; u < kDepth; ++u) x[u] = load(u);
-    // phase 1
+    // phase 1 (t = score * sign(scale), weights exp((t - max t) * |scale|))
+    const float sgn = scale < 0.0f ? -1.0f : 1.0f, sa = fabsf(scale);
     float lg[G], m[G], l[G], nan[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
@@ -2838,7 +2856,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         if (tid < nt && (uint32_t)j < group) {
             const float sc = scores[((size_t)row * group + j) * n_tok + t0 + tid];
             nan[j] = isnan(sc) ? 1.0f : 0.0f;
-            lg[j] = sc * scale;
+            lg[j] = sc * sgn;
         }
         m[j] = lg[j];
     }
@@ -2846,7 +2864,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     block_reduce_g<G, true>(nan, tmp);
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-        const float w = tid < nt ? __expf(lg[j] - m[j]) : 0.0f;
+        const float w = tid < nt ? __expf((lg[j] - m[j]) * sa) : 0.0f;
         e[j][tid] = w;
         l[j] = w;
     }
@@ -2958,6 +2976,8 @@ __global__ __launch_bounds__(256, G <= 4 ? 4 : 3) void attn_fused_kernel(const u
             score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, ew, nullptr, 64, lane);
     }
     // Softmax statistics of the wave; lane holds token wave0 + lane.
+    // t = score * sign(scale), weights exp((t - max t) * |scale|).
+    const float sgn = scale < 0.0f ? -1.0f : 1.0f, sa = fabsf(scale);
     float m[G], l[G];
     bool bad[G];
 #pragma unroll
@@ -2967,14 +2987,14 @@ __global__ __launch_bounds__(256, G <= 4 ? 4 : 3) void attn_fused_kernel(const u
         if (lane < nw && (uint32_t)j < group) {
             const float sc = ew[j * 64 + lane];
             nan_j = isnan(sc);
-            lg = sc * scale;
+            lg = sc * sgn;
         }
         bad[j] = __any(nan_j);
         float mx = lg;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
         m[j] = mx;
-        const float wgt = lane < nw ? __expf(lg - mx) : 0.0f;
+        const float wgt = lane < nw ? __expf((lg - mx) * sa) : 0.0f;
         ew[j * 64 + lane] = wgt;
         float sm = wgt;
 #pragma unroll
@@ -3057,7 +3077,7 @@ __global__ __launch_bounds__(256, G <= 4 ? 4 : 3) void attn_fused_kernel(const u
         float c[4], od[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            c[k] = wst[k][j][0] == -INFINITY ? 0.0f : __expf(wst[k][j][0] - M);
+            c[k] = wst[k][j][0] == -INFINITY ? 0.0f : __expf((wst[k][j][0] - M) * sa);
             od[k] = reinterpret_cast<const float*>(tile_lds[k])[G * 64 + j * DV + d];
         }
         float* pp = part + (((size_t)row * n_seg + seg) * group + j) * attn_partial_floats(DV);
@@ -3079,7 +3099,9 @@ __global__ __launch_bounds__(256, G <= 4 ? 4 : 3) void attn_fused_kernel(const u
 // block max, so up to 16 U segments cost one round trip to memory.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
                                                            uint32_t n_seg, uint32_t group,
-                                                           uint32_t d_v, float* __restrict__ out) {
+                                                           uint32_t d_v, float scale,
+                                                           float* __restrict__ out) {
+    const float sa = fabsf(scale);  // partial maxima are in t = score * sign(scale)
     constexpr uint32_t U = 8;
     __shared__ float red_a[4][16], red_l[4], red_m[4];
     __shared__ uint32_t red_n[4];
@@ -3112,7 +3134,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 #pragma unroll
     for (uint32_t u = 0; u < U; ++u) {
         if (sl + 16u * u < n_seg) {
-            const float f = __expf(mu[u] - M);
+            const float f = __expf((mu[u] - M) * sa);
             nan = nan || isnan(lu[u]);
             L = fmaf(lu[u], f, L);
             acc = fmaf(au[u], f, acc);
@@ -3120,7 +3142,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     }
     for (uint32_t sg = sl + 16u * U; sg < n_seg; sg += 16u) {  // more than 16 U segments
         const float* ps = p0 + sg * stride;
-        const float f = __expf(ps[0] - M);
+        const float f = __expf((ps[0] - M) * sa);
         nan = nan || isnan(ps[1]);
         L = fmaf(ps[1], f, L);
         acc = fmaf(ps[4 + d], f, acc);
@@ -3252,18 +3274,23 @@ __global__ __launch_bounds__(256) void eventlog_unpack_kernel(const uint4* __res
 // ---------------------------------------------------------------------------
 // CCOS control plane over the device arena (ccos.rs)
 
-// insert: tile i -> arena slot dst[i] with 8 lanes per tile, importance reset.
+// insert: tile i -> arena slot dst[i] with 8 lanes per tile, importance reset
+// and, with a state array, the slot's state from the tile's FLAG_WARM (1 WARM,
+// else 0 HOT; ccos.rs:226-247).
 __global__ __launch_bounds__(256) void tile_scatter_kernel(const uint4* __restrict__ src,
                                                            const uint32_t* __restrict__ dst,
                                                            uint64_t n, uint4* __restrict__ arena,
-                                                           float* __restrict__ importance) {
+                                                           float* __restrict__ importance,
+                                                           uint8_t* __restrict__ state) {
     const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (q >= n * 8) return;
     const uint64_t i = q >> 3;
     const uint32_t j = (uint32_t)(q & 7u);
     const uint32_t slot = dst[i];
-    arena[(size_t)slot * 8 + j] = src[q];
+    const uint4 v = src[q];
+    arena[(size_t)slot * 8 + j] = v;
     if (j == 0 && importance) importance[slot] = 0.0f;
+    if (j == 7 && state) state[slot] = ((v.y >> 16) & kFlagWarm) ? 1 : 0;  // flags @118
 }
 
 // observe_scores (ccos.rs:257-300) over the scores of slots [0, n), in two
@@ -3790,7 +3817,7 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
 #undef SLHA_FUSED
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, out);
+        attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, scale, out);
         return hipGetLastError();
     }
     e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr, ws + sb + pb, s);
@@ -3798,7 +3825,7 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
     const dim3 grid(n_seg, n_rows);
     e = attn_partial_dispatch(grid, scores, vals, v_dtype, n_tok, group, d_v, scale, part, s);
     if (e != hipSuccess) return e;
-    attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, out);
+    attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, scale, out);
     return hipGetLastError();
 }
 
@@ -3848,10 +3875,10 @@ hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t vers
 }
 
 hipError_t launch_tile_scatter(const void* src, const uint32_t* dst, uint64_t n, void* arena,
-                               float* importance, hipStream_t s) {
+                               float* importance, uint8_t* state, hipStream_t s) {
     if (n == 0) return hipSuccess;
     tile_scatter_kernel<<<(unsigned)((n * 8 + 255) / 256), 256, 0, s>>>(
-        static_cast<const uint4*>(src), dst, n, static_cast<uint4*>(arena), importance);
+        static_cast<const uint4*>(src), dst, n, static_cast<uint4*>(arena), importance, state);
     return hipGetLastError();
 }
 
@@ -3878,10 +3905,12 @@ hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint
     return hipGetLastError();
 }
 
-hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s) {
+hipError_t launch_ccos_apply(void* tiles, uint8_t* state, const uint32_t* slots, uint32_t slot0, uint64_t n,
+                             int op, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    ccos_apply_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<uint4*>(tiles), slots,
-                                                                 n, op);
+    if (op < 0 || op > 2 || (!slots && n != 1)) return hipErrorInvalidValue;
+    ccos_apply_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<uint4*>(tiles), state, slots,
+                                                                 slot0, n, op);
     return hipGetLastError();
 }
 

@@ -89,6 +89,11 @@ def _setup(s, torch, n_rows, n_tok, group, seed, codec=0):
     (2, 2000, 8, 128, "bf16"),
     (1, 777, 6, 64, "f32"),
     (1, 300, 16, 128, "bf16"),
+    # more than 16 x 8 = 128 segments of 256 tokens: the combine's loops past
+    # its first 128 segments, and a partial last segment
+    (1, 65537, 4, 128, "bf16"),
+    (2, 65537, 8, 64, "f32"),
+    (1, 40000, 16, 64, "bf16"),
 ])
 def test_gpu_decode_attention(s, torch, n_rows, n_tok, group, d_v, vdt):
     print(f"decode attention rows={n_rows} tok={n_tok} group={group} d_v={d_v} {vdt}", flush=True)
@@ -136,3 +141,29 @@ def test_gpu_decode_attention_degenerate(s, torch):
     empty = torch.empty((1, 0, 128), dtype=torch.uint8, device="cuda")
     out = s.gpu_decode_attention(empty, torch.empty((1, 0, 128), device="cuda"), qc, qs, group=2)
     assert (out == 0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group,d_v", [(4, 128), (8, 64), (16, 64)])
+@pytest.mark.parametrize("scale", [1e38, -1e38, 3e30, -0.5])
+def test_gpu_decode_attention_extreme_scale(s, torch, group, d_v, scale):
+    """softmax_into forms logits in f64 (metrics.rs:351-358), so a huge finite
+    scale still gives finite logits: the weights go one-hot to the top score
+    (the lowest for a negative scale), shared equally between tied tokens."""
+    print(f"decode attention scale={scale} group={group} d_v={d_v}", flush=True)
+    n_rows, n_tok = 2, 1500
+    tiles, qc, qs = _setup(s, torch, n_rows, n_tok, group, 77)
+    # ties: tokens 1000.. repeat token 0's tile, so the extreme score may be shared
+    tiles[:, 1000:1100] = tiles[:, :1].clone()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    vals = torch.randn((n_rows, n_tok, d_v), device="cuda", generator=g)
+    out = s.gpu_decode_attention(tiles, vals, qc, qs, group=group, scale=scale).cpu().numpy()
+    fast = s.gpu_score(tiles, qc, qs, group=group).cpu().numpy()
+    v_np = vals.cpu().numpy()
+    vmax = float(np.abs(v_np).max())
+    assert np.isfinite(out).all()
+    for qh in range(n_rows * group):
+        w = o.softmax(fast[qh], scale)
+        assert abs(float(w.sum()) - 1.0) < 1e-5
+        ref = o.aggregate(w, v_np[qh // group])
+        assert np.abs(out[qh] - ref).max() <= 2e-5 * vmax, qh
