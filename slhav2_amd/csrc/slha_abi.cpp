@@ -1053,7 +1053,7 @@ int32_t slha_gpu_ccos_apply(SciRustSlhaTile* tiles_dev, const uint32_t* slots_de
         if (n == 0) return;
         if (!tiles_dev || !slots_dev) fail(SLHA_ERR_NULL, "slha_gpu_ccos_apply received a NULL pointer");
         require_device();
-        check_hip(launch_ccos_apply(tiles_dev, slots_dev, n, op, static_cast<hipStream_t>(stream)),
+        check_hip(launch_ccos_apply(tiles_dev, nullptr, slots_dev, 0, n, op, static_cast<hipStream_t>(stream)),
                   "ccos kernel");
     });
 }
@@ -1514,13 +1514,6 @@ T* stage(DevBuf& b, const T* host, size_t n, hipStream_t s) {
     return d;
 }
 
-void sync_state(CcosObj* C, hipStream_t s) {
-    if (C->len() == 0) return;
-    check_hip(hipMemcpyAsync(C->state_dev, C->state.data(), C->len(), hipMemcpyHostToDevice, s),
-              "hipMemcpyAsync (CCOS state)");
-    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-}
-
 // ccos.rs:497-512
 std::vector<uint32_t> paging_order(const CcosObj* C, uint8_t st) {
     std::vector<uint32_t> v;
@@ -1535,10 +1528,14 @@ std::vector<uint32_t> paging_order(const CcosObj* C, uint8_t st) {
     return v;
 }
 
+// The device side of op 0 page_out, 1 drop_correction or 2 evict over
+// `slots`: tile bytes and the device copy of each slot's state, in one
+// launch (the slot is a kernel argument when there is one), then the
+// stream is drained, so the call returns with its work done.
 void apply_op(CcosObj* C, const std::vector<uint32_t>& slots, int op, hipStream_t s) {
     if (slots.empty()) return;
-    const uint32_t* d = stage(C->stage_a, slots.data(), slots.size(), s);
-    check_hip(launch_ccos_apply(C->arena, d, slots.size(), op, s), "ccos kernel");
+    const uint32_t* d = slots.size() == 1 ? nullptr : stage(C->stage_a, slots.data(), slots.size(), s);
+    check_hip(launch_ccos_apply(C->arena, C->state_dev, d, slots[0], slots.size(), op, s), "ccos kernel");
     check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
 
@@ -1561,42 +1558,76 @@ bool page_out_host(CcosObj* C, uint32_t s) {
     return true;
 }
 
-// evict (ccos.rs:404-438) of a batch, in order: the records go to the log in
-// one append; a failed durable append keeps the whole batch live. Returns the
-// number of slots that became COLD.
-size_t evict_batch(CcosObj* C, const std::vector<uint32_t>& slots, hipStream_t s) {
-    if (slots.empty()) return 0;
+// The eviction records of `slots` (seq, slot, tile; ccos.rs:410-420),
+// packed on the GPU and appended to the attached log in one call. Returns the
+// append's status; a failed append leaves the log as it was.
+int32_t append_evictions(CcosObj* C, const std::vector<uint32_t>& slots, hipStream_t s) {
     const size_t n = slots.size();
-    if (C->log) {
-        std::vector<uint64_t> seqs(n);
-        for (size_t i = 0; i < n; ++i) seqs[i] = C->seq[slots[i]];
-        const uint32_t* ds = stage(C->stage_a, slots.data(), n, s);
-        const uint64_t* dq = stage(C->stage_b, seqs.data(), n, s);
-        void* dr = C->stage_c.get(n * SLHA_EVENTLOG_RECORD_BYTES);
-        const uint32_t version = slha_eventlog_version(C->log);
-        if (version == 0) fail(SLHA_ERR_INVALID_HANDLE, "attached EventLog handle is no longer live");
-        check_hip(launch_eventlog_pack(C->arena, ds, dq, n, version, dr, s), "eventlog pack kernel");
-        std::vector<uint8_t> rec(n * SLHA_EVENTLOG_RECORD_BYTES);
-        check_hip(hipMemcpyAsync(rec.data(), dr, rec.size(), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
-        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-        const int32_t rc = slha_eventlog_append(C->log, rec.data(), n, C->durable ? 1 : 0);
-        if (rc != SLHA_OK) {
-            C->log_errors += n;
-            if (C->durable) {
-                C->blocked += n;
-                return 0;
-            }
-        }
-    } else if (C->durable) {
-        C->blocked += n;
-        return 0;
-    }
+    std::vector<uint64_t> seqs(n);
+    for (size_t i = 0; i < n; ++i) seqs[i] = C->seq[slots[i]];
+    const uint32_t* ds = stage(C->stage_a, slots.data(), n, s);
+    const uint64_t* dq = stage(C->stage_b, seqs.data(), n, s);
+    void* dr = C->stage_c.get(n * SLHA_EVENTLOG_RECORD_BYTES);
+    const uint32_t version = slha_eventlog_version(C->log);
+    if (version == 0) fail(SLHA_ERR_INVALID_HANDLE, "attached EventLog handle is no longer live");
+    check_hip(launch_eventlog_pack(C->arena, ds, dq, n, version, dr, s), "eventlog pack kernel");
+    std::vector<uint8_t> rec(n * SLHA_EVENTLOG_RECORD_BYTES);
+    check_hip(hipMemcpyAsync(rec.data(), dr, rec.size(), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return slha_eventlog_append(C->log, rec.data(), n, C->durable ? 1 : 0);
+}
+
+// The slots become COLD and go to the free list (ccos.rs:433-436).
+void mark_cold(CcosObj* C, const std::vector<uint32_t>& slots, hipStream_t s) {
     for (uint32_t sl : slots) {
         C->live -= C->slot_live_bytes(sl);
         C->state[sl] = kCold;
         C->free_list.push_back(sl);
     }
-    return n;
+    apply_op(C, slots, 2, s);
+}
+
+// evict (ccos.rs:404-438) of one live slot; true when it became COLD. A
+// failed append counts a log error, and under RequireDurable also a blocked
+// eviction, and then keeps the slot live.
+bool evict_one(CcosObj* C, uint32_t sl, hipStream_t s) {
+    if (C->log) {
+        if (append_evictions(C, {sl}, s) != SLHA_OK) {
+            ++C->log_errors;
+            if (C->durable) {
+                ++C->blocked;
+                return false;
+            }
+        }
+    } else if (C->durable) {
+        ++C->blocked;
+        return false;
+    }
+    mark_cold(C, {sl}, s);
+    return true;
+}
+
+// enforce_budget's last phase (ccos.rs:565-613) over the live slots in
+// eviction order: evict while over budget. The prefix whose eviction reaches
+// the budget is tried first as one append and one launch. When that append
+// fails (the log is left as it was), the slots are taken one at a time as
+// the reference takes them, so a failing record costs only itself and, under
+// RequireDurable, later slots can still reach the budget.
+void evict_in_order(CcosObj* C, const std::vector<uint32_t>& order, hipStream_t s) {
+    std::vector<uint32_t> batch;
+    uint64_t after = C->live;
+    for (uint32_t sl : order) {
+        if (after <= C->budget) break;
+        after -= C->slot_live_bytes(sl);
+        batch.push_back(sl);
+    }
+    if (batch.empty()) return;
+    if (!C->log && !C->durable) return mark_cold(C, batch, s);
+    if (C->log && append_evictions(C, batch, s) == SLHA_OK) return mark_cold(C, batch, s);
+    for (uint32_t sl : order) {
+        if (C->live <= C->budget) break;
+        evict_one(C, sl, s);
+    }
 }
 
 // insert_with_state (ccos.rs:226-247) of tiles already read to the host;
@@ -1711,8 +1742,9 @@ int32_t slha_ccos_insert(SlhaCcos* c, const SciRustSlhaTile* tiles_dev, size_t n
         check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
         const std::vector<uint32_t> slots = insert_host(C, host.data(), n);
         const uint32_t* d = stage(C->stage_a, slots.data(), n, s);
-        check_hip(launch_tile_scatter(tiles_dev, d, n, C->arena, C->importance, s), "tile scatter kernel");
-        sync_state(C, s);
+        check_hip(launch_tile_scatter(tiles_dev, d, n, C->arena, C->importance, C->state_dev, s),
+                  "tile scatter kernel");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
         std::memcpy(slots_out, slots.data(), n * sizeof(uint32_t));
     });
 }
@@ -1737,7 +1769,6 @@ int32_t slha_ccos_enforce_budget(SlhaCcos* c, int32_t* within_out, void* stream)
         const hipStream_t s = static_cast<hipStream_t>(stream);
         auto within = [&] { return C->live <= C->budget; };
         auto finish = [&] {
-            sync_state(C, s);
             if (within_out) *within_out = within() ? 1 : 0;
         };
         if (within()) return finish();
@@ -1776,15 +1807,7 @@ int32_t slha_ccos_enforce_budget(SlhaCcos* c, int32_t* within_out, void* stream)
                 return C->seq[a] < C->seq[b];
             });
         }
-        // The prefix whose eviction reaches the budget, evicted as one batch.
-        std::vector<uint32_t> batch;
-        uint64_t after = C->live;
-        for (uint32_t sl : live) {
-            if (after <= C->budget) break;
-            after -= C->slot_live_bytes(sl);
-            batch.push_back(sl);
-        }
-        evict_batch(C, batch, s);
+        evict_in_order(C, live, s);
         finish();
     });
 }
@@ -1795,7 +1818,6 @@ int32_t slha_ccos_page_out(SlhaCcos* c, uint32_t slot, void* stream) {
         if (slot >= C->len()) fail(SLHA_ERR_DIMENSION, "slot %u out of range", slot);
         const hipStream_t s = static_cast<hipStream_t>(stream);
         if (page_out_host(C, slot)) apply_op(C, {slot}, 0, s);
-        sync_state(C, s);
     });
 }
 
@@ -1812,10 +1834,8 @@ int32_t slha_ccos_drop_correction(SlhaCcos* c, uint32_t slot, int32_t* done_out,
 int32_t slha_ccos_evict(SlhaCcos* c, uint32_t slot, int32_t* done_out, void* stream) {
     return ffi_status([&] {
         CcosObj* C = ccos_of(c);
-        size_t done = 0;
-        const hipStream_t s = static_cast<hipStream_t>(stream);
-        if (slot < C->len() && C->state[slot] != kCold) done = evict_batch(C, {slot}, s);
-        sync_state(C, s);
+        bool done = false;
+        if (slot < C->len() && C->state[slot] != kCold) done = evict_one(C, slot, static_cast<hipStream_t>(stream));
         if (done_out) *done_out = done ? 1 : 0;
     });
 }
@@ -1837,8 +1857,8 @@ int32_t slha_ccos_rehydrate(SlhaCcos* c, uint64_t seq, int64_t* slot_out, void* 
         const std::vector<uint32_t> slots = insert_host(C, rec + 16, 1);
         const uint8_t* dt = stage(C->stage_b, rec + 16, 128, s);
         const uint32_t* d = stage(C->stage_a, slots.data(), 1, s);
-        check_hip(launch_tile_scatter(dt, d, 1, C->arena, C->importance, s), "tile scatter kernel");
-        sync_state(C, s);
+        check_hip(launch_tile_scatter(dt, d, 1, C->arena, C->importance, C->state_dev, s), "tile scatter kernel");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
         *slot_out = slots[0];
     });
 }

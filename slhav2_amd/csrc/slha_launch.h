@@ -92,17 +92,22 @@ size_t decode_attention_workspace_bytes(uint32_t n_rows, uint32_t n_tok, uint32_
 hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, float sqrt_half_pi,
                          float* out, hipStream_t s);
 hipError_t launch_validate(const void* tiles, uint64_t n, uint64_t* status, hipStream_t s);
-hipError_t launch_ccos_apply(void* tiles, const uint32_t* slots, uint64_t n, int op, hipStream_t s);
+// op 0 page_out, 1 drop_correction, 2 evict (state only) over slots[0, n), or
+// over the one slot `slot0` when slots is NULL (n = 1); page_out and evict
+// write the new state into `state` when it is non-NULL.
+hipError_t launch_ccos_apply(void* tiles, uint8_t* state, const uint32_t* slots, uint32_t slot0, uint64_t n,
+                             int op, hipStream_t s);
 // EventLog records (144 B each, eventlog.rs:9-36); n < 2^31 * 256.
 hipError_t launch_eventlog_pack(const void* arena, const uint32_t* slots, const uint64_t* seqs,
                                 uint64_t n, uint32_t version, void* records, hipStream_t s);
 hipError_t launch_eventlog_unpack(const void* records, uint64_t n, uint32_t version,
                                   const uint32_t* dst, void* arena, uint32_t* status, hipStream_t s);
-// CCOS: tile i -> arena slot dst[i] (importance[dst[i]] = 0 when non-NULL);
+// CCOS: tile i -> arena slot dst[i] (importance[dst[i]] = 0 and state[dst[i]]
+// from the tile's FLAG_WARM, each when non-NULL);
 // observe_scores over scores[0, n) with state (0 HOT, 1 WARM, 2 COLD) and a
 // workspace of observe_workspace_floats() floats.
 hipError_t launch_tile_scatter(const void* src, const uint32_t* dst, uint64_t n, void* arena,
-                               float* importance, hipStream_t s);
+                               float* importance, uint8_t* state, hipStream_t s);
 size_t observe_workspace_floats();
 hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint64_t n, float temperature,
                                  float* importance, float* workspace, hipStream_t s);

@@ -388,6 +388,43 @@ def test_durable_eviction_persists_and_failure_keeps_tile_live(sa, torch, tmp_pa
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("durable", [True, False])
+def test_failed_appends_evict_slot_by_slot(sa, torch, tmp_path, durable):
+    """enforce_budget's eviction loop (ccos.rs:596-611) calls evict
+    (ccos.rs:404-438) one slot at a time. With a log that refuses every
+    append and three WARM slots (288 B) over a 200 B budget, one eviction
+    would do: under RequireDurable every live slot is tried and blocked
+    (3 log errors, 3 blocked, nothing evicted); best effort evicts the first
+    slot after its failed append (1 log error, 0 blocked)."""
+    q = tmp_path / "ro"
+    sa.EventLog.create(q).close()
+    ro = sa.EventLog.open_read_only(q)
+    c = sa.ElasticKvCache(arena(torch, 8), 200, policy=sa.PAGE_OLDEST_FIRST)
+    (c.attach_durable_event_log if durable else c.attach_event_log)(ro)
+    slots = c.insert(tiles_of(sa, torch, 3, seed=31))
+    within = c.enforce_budget()
+    if durable:
+        assert not within and c.counts() == (0, 3, 0)
+        assert (c.log_errors(), c.blocked_evictions()) == (3, 3)
+    else:
+        assert within and c.counts() == (0, 2, 1) and c.state(slots[0]) == sa.COLD
+        assert (c.log_errors(), c.blocked_evictions()) == (1, 0)
+    # the device copy of the states follows every change: observe_scores
+    # skips exactly the COLD slots, also after a recycled insert
+    t = tiles_of(sa, torch, 2, seed=32)
+    c.insert(t[:1])
+    live = (c._slots()[0] != sa.COLD).astype(np.uint8)
+    sc = np.array([1.0, 2.0, 3.0, 4.0][:len(c)], np.float32)
+    c.observe_scores(torch.from_numpy(sc).cuda(), 1.0)
+    want = o.observe_scores(np.zeros(len(c), np.float32), sc, live, 1.0)
+    np.testing.assert_allclose(c._slots()[2], want, rtol=1e-5, atol=1e-8)
+    with sa.EventLog.open(q) as r:
+        assert len(r) == 0
+    ro.close()
+    c.close()
+
+
+@pytest.mark.gpu
 def test_evict_snapshots_to_event_log_then_rehydrates_identically(sa, torch, tmp_path):
     """tests/ccos.rs:689-747 and 750-767."""
     p = tmp_path / "rt"
