@@ -141,6 +141,27 @@ int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_
                                   float* topk_score_dev, void* stream);
 
 /*
+ * slha_gpu_score_paged_topk without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and outputs as slha_gpu_score_paged_topk. The top-k
+ * candidate lists (n_seq * n_kv_heads * group * ceil(max_len / 16384) * k * 8
+ * bytes) live in a library-owned static device array of
+ * SLHA_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends; a
+ * call needing more returns SLHA_ERR_DIMENSION before any device work. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.
+ */
+#define SLHA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int32_t slha_gpu_score_paged_topk_noalloc(const SciRustSlhaTile* arena_dev, size_t page_tiles,
+                                          const uint32_t* page_table_dev, size_t max_pages,
+                                          const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
+                                          size_t n_seq, size_t max_len, size_t n_kv_heads, size_t group,
+                                          const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                          float* scores_dev, size_t k, uint32_t* topk_idx_dev,
+                                          float* topk_score_dev, void* stream);
+
+/*
  * Decode attention over compressed keys (the decode step of
  * scirust/examples/benchmark_decode.rs:29-90): for query head
  * qh = r*group + j of row r,

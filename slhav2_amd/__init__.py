@@ -121,6 +121,8 @@ _SIGS = {
     "slha_gpu_decode": (_I32, [_P, _P, _SZ, _I32, _P, _P]),
     "slha_gpu_score_paged_topk": (_I32, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P,
                                          _P, _SZ, _P, _P, _P]),
+    "slha_gpu_score_paged_topk_noalloc": (_I32, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P,
+                                                 _P, _P, _SZ, _P, _P, _P]),
     "slha_gpu_ccos_apply": (_I32, [_P, _P, _SZ, _I32, _P]),
     "slha_gpu_decode_attention": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _P, _P, _SZ, ctypes.c_float,
                                          _P, _P]),
@@ -475,11 +477,14 @@ def gpu_ccos_apply(tiles, slots, op: int, stream=None) -> None:
 
 def gpu_score_paged_topk(arena, page_tiles: int, page_table, max_pages: int, seq_len,
                          n_kv_heads: int, group: int, q_coarse, q_sign, k: int,
-                         max_len: int | None = None, scores=None, stream=None):
+                         max_len: int | None = None, scores=None, stream=None,
+                         noalloc: bool = False):
     """Paged CCOS scoring + top-k. seq_len: int32 GPU tensor [n_seq].
 
     Returns (scores f32 flat, topk_idx int32 [n_seq, Hq, k], topk_val f32 [n_seq, Hq, k]);
     scores of sequence s start at score_base[s] = Hq * sum(seq_len[:s]).
+    noalloc=True calls slha_gpu_score_paged_topk_noalloc (the library
+    allocates nothing; the outputs here are still torch tensors).
     """
     import torch
 
@@ -496,7 +501,8 @@ def gpu_score_paged_topk(arena, page_tiles: int, page_table, max_pages: int, seq
         scores = torch.empty(max(total, 1), dtype=torch.float32, device=seq_len.device)
     idx = torch.empty((n_seq, hq, max(k, 1)), dtype=torch.int32, device=seq_len.device)
     val = torch.empty((n_seq, hq, max(k, 1)), dtype=torch.float32, device=seq_len.device)
-    _check(lib.slha_gpu_score_paged_topk(
+    fn = lib.slha_gpu_score_paged_topk_noalloc if noalloc else lib.slha_gpu_score_paged_topk
+    _check(fn(
         _dev_ptr(arena), page_tiles, _dev_ptr(page_table), max_pages, _dev_ptr(seq_len),
         _dev_ptr(base), n_seq, max_len, n_kv_heads, group, _dev_ptr(q_coarse), _dev_ptr(q_sign),
         _dev_ptr(scores), k, _dev_ptr(idx), _dev_ptr(val), _stream(stream)))

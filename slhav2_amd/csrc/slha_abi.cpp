@@ -1003,6 +1003,44 @@ int32_t slha_gpu_decode(const SlhaModel* model, const SciRustSlhaTile* tiles_dev
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by the two paged entry points; returns log2(page_tiles),
+// or -1 when there is no work (n_seq == 0 or max_len == 0).
+int paged_checks(const SciRustSlhaTile* arena_dev, size_t page_tiles, const uint32_t* page_table_dev,
+                 size_t max_pages, const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
+                 size_t n_seq, size_t max_len, size_t n_kv_heads, size_t group,
+                 const float* q_coarse_dev, const uint64_t* q_sign_dev, float* scores_dev, size_t k,
+                 uint32_t* topk_idx_dev, float* topk_score_dev, const char* fn) {
+    if (page_tiles == 0 || (page_tiles & (page_tiles - 1)) != 0 || page_tiles > (1u << 30))
+        fail(SLHA_ERR_DIMENSION, "page_tiles=%zu must be a power of two", page_tiles);
+    if (group == 0 || group > kMaxGroup)
+        fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
+    if (k > kMaxTopK) fail(SLHA_ERR_DIMENSION, "k=%zu exceeds %u", k, kMaxTopK);
+    if (k > 0 && (max_len + kTopkSeg - 1) / kTopkSeg * k > kTopkMaxCandidates)
+        fail(SLHA_ERR_DIMENSION,
+             "top-k of rows up to max_len=%zu needs ceil(max_len/%u)*k <= %u (k=%zu)",
+             max_len, kTopkSeg, kTopkMaxCandidates, k);
+    if (n_kv_heads == 0 || n_seq * n_kv_heads > 65535 || max_len > 0xFFFFFFFFull ||
+        max_pages > 0xFFFFFFFFull || (uint64_t)max_len > (uint64_t)max_pages * page_tiles)
+        fail(SLHA_ERR_DIMENSION, "paged geometry out of range (n_seq=%zu n_kv=%zu max_len=%zu)",
+             n_seq, n_kv_heads, max_len);
+    if (n_seq == 0 || max_len == 0) return -1;
+    if (!arena_dev || !page_table_dev || !seq_len_dev || !score_base_dev || !q_coarse_dev ||
+        !q_sign_dev || !scores_dev || (k > 0 && (!topk_idx_dev || !topk_score_dev)))
+        fail(SLHA_ERR_NULL, "%s received a NULL pointer", fn);
+    require_device();
+    int shift = 0;
+    while ((size_t(1) << shift) < page_tiles) ++shift;
+    return shift;
+}
+
+}  // namespace
+
+extern "C" {
+
 int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_tiles,
                                   const uint32_t* page_table_dev, size_t max_pages,
                                   const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
@@ -1011,37 +1049,56 @@ int32_t slha_gpu_score_paged_topk(const SciRustSlhaTile* arena_dev, size_t page_
                                   float* scores_dev, size_t k, uint32_t* topk_idx_dev,
                                   float* topk_score_dev, void* stream) {
     return ffi_status([&] {
-        if (page_tiles == 0 || (page_tiles & (page_tiles - 1)) != 0 || page_tiles > (1u << 30))
-            fail(SLHA_ERR_DIMENSION, "page_tiles=%zu must be a power of two", page_tiles);
-        if (group == 0 || group > kMaxGroup)
-            fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
-        if (k > kMaxTopK) fail(SLHA_ERR_DIMENSION, "k=%zu exceeds %u", k, kMaxTopK);
-        if (k > 0 && (max_len + kTopkSeg - 1) / kTopkSeg * k > kTopkMaxCandidates)
-            fail(SLHA_ERR_DIMENSION,
-                 "top-k of rows up to max_len=%zu needs ceil(max_len/%u)*k <= %u (k=%zu)",
-                 max_len, kTopkSeg, kTopkMaxCandidates, k);
-        if (n_kv_heads == 0 || n_seq * n_kv_heads > 65535 || max_len > 0xFFFFFFFFull ||
-            max_pages > 0xFFFFFFFFull || (uint64_t)max_len > (uint64_t)max_pages * page_tiles)
-            fail(SLHA_ERR_DIMENSION, "paged geometry out of range (n_seq=%zu n_kv=%zu max_len=%zu)",
-                 n_seq, n_kv_heads, max_len);
-        if (n_seq == 0 || max_len == 0) return;
-        if (!arena_dev || !page_table_dev || !seq_len_dev || !score_base_dev || !q_coarse_dev ||
-            !q_sign_dev || !scores_dev || (k > 0 && (!topk_idx_dev || !topk_score_dev)))
-            fail(SLHA_ERR_NULL, "slha_gpu_score_paged_topk received a NULL pointer");
-        require_device();
-        uint32_t shift = 0;
-        while ((size_t(1) << shift) < page_tiles) ++shift;
+        const int shift = paged_checks(arena_dev, page_tiles, page_table_dev, max_pages, seq_len_dev,
+                                       score_base_dev, n_seq, max_len, n_kv_heads, group, q_coarse_dev,
+                                       q_sign_dev, scores_dev, k, topk_idx_dev, topk_score_dev,
+                                       "slha_gpu_score_paged_topk");
+        if (shift < 0) return;
         hipStream_t s = static_cast<hipStream_t>(stream);
         void* ws = k == 0 ? nullptr
                           : stream_workspace(paged_topk_workspace_bytes(
                                                  (uint32_t)n_seq, (uint32_t)max_len,
                                                  (uint32_t)n_kv_heads, (uint32_t)group, (uint32_t)k),
                                              s);
-        check_hip(launch_score_paged_topk(arena_dev, shift, page_table_dev, (uint32_t)max_pages,
+        check_hip(launch_score_paged_topk(arena_dev, (uint32_t)shift, page_table_dev, (uint32_t)max_pages,
                                           seq_len_dev, score_base_dev, (uint32_t)n_seq,
                                           (uint32_t)max_len, (uint32_t)n_kv_heads, (uint32_t)group,
                                           q_coarse_dev, q_sign_dev, scores_dev, (uint32_t)k,
                                           topk_idx_dev, topk_score_dev, ws, s),
+                  "paged score kernel");
+    });
+}
+
+static_assert(SLHA_NOALLOC_SCRATCH_BYTES == kNoAllocScratchBytes, "header and library agree on the scratch size");
+
+int32_t slha_gpu_score_paged_topk_noalloc(const SciRustSlhaTile* arena_dev, size_t page_tiles,
+                                          const uint32_t* page_table_dev, size_t max_pages,
+                                          const uint32_t* seq_len_dev, const uint64_t* score_base_dev,
+                                          size_t n_seq, size_t max_len, size_t n_kv_heads, size_t group,
+                                          const float* q_coarse_dev, const uint64_t* q_sign_dev,
+                                          float* scores_dev, size_t k, uint32_t* topk_idx_dev,
+                                          float* topk_score_dev, void* stream) {
+    return ffi_status([&] {
+        const int shift = paged_checks(arena_dev, page_tiles, page_table_dev, max_pages, seq_len_dev,
+                                       score_base_dev, n_seq, max_len, n_kv_heads, group, q_coarse_dev,
+                                       q_sign_dev, scores_dev, k, topk_idx_dev, topk_score_dev,
+                                       "slha_gpu_score_paged_topk_noalloc");
+        if (shift < 0) return;
+        const size_t need = k == 0 ? 0
+                                   : paged_topk_workspace_bytes((uint32_t)n_seq, (uint32_t)max_len,
+                                                                (uint32_t)n_kv_heads, (uint32_t)group,
+                                                                (uint32_t)k);
+        if (need > kNoAllocScratchBytes)
+            fail(SLHA_ERR_DIMENSION,
+                 "top-k candidates need %zu bytes (n_seq*n_kv*group*ceil(max_len/%u)*k*8); the "
+                 "no-allocation entry point holds %zu",
+                 need, kTopkSeg, kNoAllocScratchBytes);
+        check_hip(launch_score_paged_topk_noalloc(arena_dev, (uint32_t)shift, page_table_dev,
+                                                  (uint32_t)max_pages, seq_len_dev, score_base_dev,
+                                                  (uint32_t)n_seq, (uint32_t)max_len, (uint32_t)n_kv_heads,
+                                                  (uint32_t)group, q_coarse_dev, q_sign_dev, scores_dev,
+                                                  (uint32_t)k, topk_idx_dev, topk_score_dev,
+                                                  static_cast<hipStream_t>(stream)),
                   "paged score kernel");
     });
 }

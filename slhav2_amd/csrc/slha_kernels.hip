@@ -23,6 +23,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace slha {
 
@@ -3567,6 +3568,56 @@ size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_k
     const size_t rows = (size_t)n_seq * n_kv * group;
     const size_t nseg = (max_len + kTopkSeg - 1) / kTopkSeg;
     return rows * nseg * k * 2 * sizeof(uint32_t);
+}
+
+// Paged scoring + top-k that allocates nothing: the top-k candidate lists
+// live in `scratch`, a file-scope device array of kNoAllocScratchBytes that
+// every GPU the library runs on holds until the process ends. Its device
+// address is looked up once per device (hipGetSymbolAddress with that device
+// current) and kept; the array's name is never passed to a kernel. The
+// segment kernel writes every list entry the merge reads in the same call,
+// so the array needs no clearing between calls. Calls that overlap on one GPU
+// (two streams, two threads) share the array and race.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kScratchMaxDevices];
+}  // namespace
+
+hipError_t noalloc_scratch(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kScratchMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+
+hipError_t launch_score_paged_topk_noalloc(const void* arena, uint32_t page_shift,
+                                          const uint32_t* page_table, uint32_t max_pages,
+                                          const uint32_t* seq_len, const uint64_t* score_base,
+                                          uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
+                                          uint32_t group, const float* qc, const uint64_t* qs,
+                                          float* scores, uint32_t k, uint32_t* topk_idx,
+                                          float* topk_val, hipStream_t s) {
+    void* ws = nullptr;
+    if (k > 0 && n_seq > 0 && max_len > 0) {
+        if (paged_topk_workspace_bytes(n_seq, max_len, n_kv, group, k) > kNoAllocScratchBytes)
+            return hipErrorInvalidValue;  // checked by the ABI with its own message
+        const hipError_t e = noalloc_scratch(&ws);
+        if (e != hipSuccess) return e;
+    }
+    return launch_score_paged_topk(arena, page_shift, page_table, max_pages, seq_len, score_base, n_seq,
+                                   max_len, n_kv, group, qc, qs, scores, k, topk_idx, topk_val, ws, s);
 }
 
 namespace {

@@ -37,6 +37,18 @@ hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
 // Device bytes of the `workspace` launch_score_paged_topk needs (top-k candidates).
 size_t paged_topk_workspace_bytes(uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
                                   uint32_t group, uint32_t k);
+// The same launch with the candidate lists in a file-scope device array of
+// kNoAllocScratchBytes (16 MiB: C5, 2048 query rows of up to 131 072 tokens at
+// k = 64, takes 8 MiB); nothing is allocated. hipErrorInvalidValue when
+// paged_topk_workspace_bytes() exceeds it.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+hipError_t launch_score_paged_topk_noalloc(const void* arena, uint32_t page_shift,
+                                          const uint32_t* page_table, uint32_t max_pages,
+                                          const uint32_t* seq_len, const uint64_t* score_base,
+                                          uint32_t n_seq, uint32_t max_len, uint32_t n_kv,
+                                          uint32_t group, const float* qc, const uint64_t* qs,
+                                          float* scores, uint32_t k, uint32_t* topk_idx,
+                                          float* topk_val, hipStream_t s);
 // Mode R computes the sign sketch on MFMA when `zpack` (build_projection_pack)
 // is given, else sequentially per lane; both give the reference's bits.
 hipError_t launch_encode(const void* keys, int dtype, uint64_t n_keys, uint32_t n_tok,
