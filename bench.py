@@ -40,7 +40,7 @@ PAIRS = N_Q * N_TOK
 ROTATION = 10
 PEAK_HBM_GBS = 8000.0
 TILE_BYTES = 128
-SCORE_KERNEL = "slha::score_rows_fast_kernel<4u>"
+SCORE_KERNEL = "slha::score_rows_int4_kernel"
 PROFILES = ROOT / "profiles"
 COPY_BYTES = 1 << 30
 
@@ -656,23 +656,31 @@ def main() -> int:
 
     # Steps call the C ABI directly with prebuilt arguments (the Python
     # wrapper's checks cost about as much host time as the kernel itself).
-    score = s.lib.slha_gpu_score
+    # The tiles were encoded with codec 0 (INT4), and the call says so
+    # (slha_gpu_score_codec), which selects the integer INT4 kernel.
+    score = s.lib.slha_gpu_score_codec
     vp = ctypes.c_void_p
     sargs = [(vp(sets[k].data_ptr()), N_KV, N_TOK, vp(qc.data_ptr()), vp(qs.data_ptr()), GROUP,
-              s.SCORE_FAST, vp(outs[k].data_ptr()), None, vp(stream.cuda_stream))
+              s.SCORE_FAST, s.CODEC_INT4_SINGLE, vp(outs[k].data_ptr()), None, vp(stream.cuda_stream))
              for k in range(ROTATION)]
 
     def step(i: int) -> None:
         rc = score(*sargs[i % ROTATION])
         if rc != 0:
-            raise RuntimeError(f"slha_gpu_score failed: {rc} {s.last_error()}")
+            raise RuntimeError(f"slha_gpu_score_codec failed: {rc} {s.last_error()}")
 
-    # the fast path of the C ABI must agree with the Python wrapper
-    ref = s.gpu_score(sets[0], qc, qs, group=GROUP, stream=stream)
+    # the fast path of the C ABI must agree with the Python wrapper, and the
+    # scores with the exact (reference-order) path within the fast tolerance
+    ref = s.gpu_score(sets[0], qc, qs, group=GROUP, stream=stream, codec_hint=s.CODEC_INT4_SINGLE)
     step(0)
     torch.cuda.synchronize()
     if not torch.equal(ref, outs[0]):
         raise RuntimeError("direct C-ABI launch disagrees with gpu_score")
+    exact = s.gpu_score(sets[0], qc, qs, group=GROUP, mode=s.SCORE_EXACT, stream=stream)
+    err = ((outs[0] - exact).abs() / (1 + exact.abs())).max().item()
+    if not err <= 1e-3:
+        raise RuntimeError(f"C2 fast scores differ from the exact path: {err}")
+    del exact
 
     for i in range(args.warmup):
         step(i)

@@ -97,6 +97,21 @@ int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n
                        int32_t mode, float* scores_dev, uint32_t* hamming_dev, void* stream);
 
 /*
+ * slha_gpu_score with the codec the caller encoded the tiles with
+ * (SLHA_CODEC_*, or -1 if unknown; slha_gpu_score passes -1). The hint picks
+ * kernels and never changes a result: tiles of another codec are still
+ * scored by their own codec, only more slowly. With SLHA_CODEC_INT4 and
+ * group <= 4 in SLHA_SCORE_FAST mode the scores come from the integer matrix
+ * cores (queries carried to ~2^-23 relative, within the fast-mode tolerance).
+ * No counterpart in the reference, which dispatches per tile on its flags
+ * (simd.rs:23-84); an unknown hint is SLHA_ERR_CODEC.
+ */
+int32_t slha_gpu_score_codec(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
+                             const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
+                             int32_t mode, int32_t codec_hint, float* scores_dev,
+                             uint32_t* hamming_dev, void* stream);
+
+/*
  * Validate n tiles on the device (slha-c/src/lib.rs:244-286). status_dev[0]
  * receives 0, or the lowest failing tile index + 1 (u64); the failing status
  * (SLHA_ERR_NONFINITE / SLHA_ERR_INVALID_TILE) is status_dev[1].

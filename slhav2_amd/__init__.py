@@ -117,6 +117,7 @@ _SIGS = {
     "slha_gpu_encode": (_I32, [_P, _P, _I32, _SZ, _SZ, _SZ, _U32, _I32, _I32, _P, _P]),
     "slha_gpu_prepare_queries": (_I32, [_P, _P, _I32, _SZ, _P, _P, _P]),
     "slha_gpu_score": (_I32, [_P, _SZ, _SZ, _P, _P, _SZ, _I32, _P, _P, _P]),
+    "slha_gpu_score_codec": (_I32, [_P, _SZ, _SZ, _P, _P, _SZ, _I32, _I32, _P, _P, _P]),
     "slha_gpu_validate_tiles": (_I32, [_P, _SZ, _P, _P]),
     "slha_gpu_decode": (_I32, [_P, _P, _SZ, _I32, _P, _P]),
     "slha_gpu_score_paged_topk": (_I32, [_P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P,
@@ -405,8 +406,10 @@ def gpu_prepare_queries(model: Model, q, stream=None):
 
 
 def gpu_score(tiles, q_coarse, q_sign, group: int = 1, mode: int = SCORE_FAST,
-              hamming: bool = False, out=None, stream=None):
-    """tiles uint8 [n_rows, n_tok, 128]; q_* [n_rows*group, ...] -> scores f32 [n_rows*group, n_tok]."""
+              hamming: bool = False, out=None, stream=None, codec_hint: int | None = None):
+    """tiles uint8 [n_rows, n_tok, 128]; q_* [n_rows*group, ...] -> scores f32 [n_rows*group, n_tok].
+    codec_hint: the CODEC_* the tiles were encoded with (slha_gpu_score_codec);
+    it selects kernels only."""
     import torch
 
     t = tiles if tiles.dim() == 3 else tiles.unsqueeze(0)
@@ -416,8 +419,13 @@ def gpu_score(tiles, q_coarse, q_sign, group: int = 1, mode: int = SCORE_FAST,
     if out is None:
         out = torch.empty((n_rows * group, n_tok), dtype=torch.float32, device=t.device)
     ham = torch.empty((n_rows * group, n_tok), dtype=torch.int32, device=t.device) if hamming else None
-    _check(lib.slha_gpu_score(_dev_ptr(t), n_rows, n_tok, _dev_ptr(q_coarse), _dev_ptr(q_sign),
-                              group, mode, _dev_ptr(out), _dev_ptr(ham), _stream(stream)))
+    if codec_hint is None:
+        _check(lib.slha_gpu_score(_dev_ptr(t), n_rows, n_tok, _dev_ptr(q_coarse), _dev_ptr(q_sign),
+                                  group, mode, _dev_ptr(out), _dev_ptr(ham), _stream(stream)))
+    else:
+        _check(lib.slha_gpu_score_codec(_dev_ptr(t), n_rows, n_tok, _dev_ptr(q_coarse),
+                                        _dev_ptr(q_sign), group, mode, int(codec_hint), _dev_ptr(out),
+                                        _dev_ptr(ham), _stream(stream)))
     return (out, ham) if hamming else out
 
 

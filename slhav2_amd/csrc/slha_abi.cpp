@@ -489,7 +489,7 @@ void score_host_tiles(const SciRustSlhaTile* tiles, size_t n, const float* qc, c
     check_hip(hipMemcpyAsync(td, tiles, n * sizeof(SciRustSlhaTile), hipMemcpyHostToDevice, s), "H2D tiles");
     check_hip(hipMemcpyAsync(qcd, qc, 128 * sizeof(float), hipMemcpyHostToDevice, s), "H2D q_coarse");
     check_hip(hipMemcpyAsync(qsd, qs, 4 * sizeof(uint64_t), hipMemcpyHostToDevice, s), "H2D q_sign");
-    check_hip(launch_score_rows(td, 1, (uint32_t)n, 1, qcd, qsd, true, sd, nullptr, nullptr, s),
+    check_hip(launch_score_rows(td, 1, (uint32_t)n, 1, qcd, qsd, true, sd, nullptr, nullptr, -1, s),
               "score kernel");
     check_hip(hipMemcpyAsync(out, sd, n * sizeof(float), hipMemcpyDeviceToHost, s), "D2H scores");
     check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -946,9 +946,19 @@ int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int3
 int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
                        const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
                        int32_t mode, float* scores_dev, uint32_t* hamming_dev, void* stream) {
+    return slha_gpu_score_codec(tiles_dev, n_rows, n_tok, q_coarse_dev, q_sign_dev, group, mode,
+                                -1, scores_dev, hamming_dev, stream);
+}
+
+int32_t slha_gpu_score_codec(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
+                             const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
+                             int32_t mode, int32_t codec_hint, float* scores_dev,
+                             uint32_t* hamming_dev, void* stream) {
     return ffi_status([&] {
         if (mode != SLHA_SCORE_FAST && mode != SLHA_SCORE_EXACT)
             fail(SLHA_ERR_DIMENSION, "unknown score mode %d", mode);
+        if (codec_hint < -1 || codec_hint > SLHA_CODEC_MIX3)
+            fail(SLHA_ERR_CODEC, "unknown codec hint %d", codec_hint);
         if (group == 0 || group > kMaxGroup)
             fail(SLHA_ERR_DIMENSION, "group=%zu must be in [1, %u]", group, kMaxGroup);
         if (n_rows > 65535 || n_tok > 0xFFFFFFFFull)
@@ -964,7 +974,7 @@ int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n
                                     hs);
         check_hip(launch_score_rows(tiles_dev, (uint32_t)n_rows, (uint32_t)n_tok, (uint32_t)group,
                                     q_coarse_dev, q_sign_dev, mode == SLHA_SCORE_EXACT, scores_dev,
-                                    hamming_dev, ws, hs),
+                                    hamming_dev, ws, codec_hint, hs),
                   "score kernel");
     });
 }

@@ -524,7 +524,9 @@ template <uint32_t ROWS>
 __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t qrow0,
                                             uint32_t group, QueryRegs<ROWS>& r) {
     // Buffer loads over exactly the row's `group` queries: rows past `group`
-    // fall outside the range and read as zero, with no branch or clamp.
+    // fall outside the range and read as zero, with no branch or clamp. The
+    // whole offset goes in the VGPR operand: the range check of a raw buffer
+    // load does not cover the SGPR offset.
     constexpr uint32_t NA = ROWS * 32 / 256 > 0 ? ROWS * 32 / 256 : 1;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -542,21 +544,27 @@ __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t
     for (uint32_t k = 0; k < ROWS / 4; ++k) {
         const uint32_t soff = (wv + 4u * k) * kDC * 4u;
         r.b[k] = make_float2(
-            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff, soff, 0)),
-            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff + 16u, soff, 0)));
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, soff + voff, 0, 0)),
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, soff + voff + 16u, 0, 0)));
     }
 }
 
-// v0 = q_j[d], v1 = q_j[d + 4] with d = f16_stage_dim(lane); one wave per query.
-__device__ __forceinline__ void stage_f16_row(float v0, float v1, uint32_t j, uint16_t* qh,
-                                              float* qexp) {
-    const uint32_t lane = threadIdx.x & 63u;
+// Exponent e of the smallest power of two >= max |q| over the wave's query
+// (m = 0 -> e = 0); v0, v1 are this lane's two values.
+__device__ __forceinline__ int stage_exponent(float v0, float v1) {
     const float m = wave_max_nonneg(fmaxf(fabsf(v0), fabsf(v1)));
-    int e = 0;  // smallest power of two >= m (m = 0 -> 1)
+    int e = 0;
     if (m > 0.0f) {
         (void)frexpf(m, &e);
         if (ldexpf(1.0f, e - 1) == m) e -= 1;
     }
+    return e;
+}
+
+// v0 = q_j[d], v1 = q_j[d + 4] with d = f16_stage_dim(lane); one wave per query.
+__device__ __forceinline__ void stage_f16_row_e(float v0, float v1, int e, uint32_t j,
+                                                uint16_t* qh, float* qexp) {
+    const uint32_t lane = threadIdx.x & 63u;
     const float inv = ldexpf(1.0f, -e);
     const float d0 = v0 * inv, d1 = v1 * inv;
     // Truncating f16 split: x - hi is exact in f32 and lo keeps 11 more bits.
@@ -571,6 +579,11 @@ __device__ __forceinline__ void stage_f16_row(float v0, float v1, uint32_t j, ui
                  "v"(__builtin_bit_cast(uint32_t, hi)), "v"(__builtin_bit_cast(uint32_t, lo))
                  : "memory");
     if (lane == 0) qexp[j] = ldexpf(1.0f, e);
+}
+
+__device__ __forceinline__ void stage_f16_row(float v0, float v1, uint32_t j, uint16_t* qh,
+                                              float* qexp) {
+    stage_f16_row_e(v0, v1, stage_exponent(v0, v1), j, qh, qexp);
 }
 
 __device__ __forceinline__ void stage_queries_f16(const float* __restrict__ qc, size_t qrow0,
@@ -652,11 +665,13 @@ __device__ __forceinline__ void fetch_tiles_lds(const uint4* wave_base, uint32_t
     const uint32_t bytes = __builtin_amdgcn_readfirstlane((n_valid < 64u ? n_valid : 64u) * 128u);
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(wave_base), 0, bytes, 0x00020000);
+    // The whole offset in the VGPR operand: the range check of a raw buffer
+    // load covers it but not the SGPR offset.
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rsrc, (__attribute__((address_space(3))) void*)(region + 64 * j), 16, in_tile * 16u,
-            1024 * j, 0, kCachePolicyNT);
+            rsrc, (__attribute__((address_space(3))) void*)(region + 64 * j), 16,
+            1024u * j + in_tile * 16u, 0, 0, kCachePolicyNT);
 }
 
 // Lane l reads tile l back from a region filled by fetch_tiles_lds; the XOR
@@ -693,6 +708,193 @@ __global__ __launch_bounds__(256) void score_rows_kernel(
     if (!valid) return;
     score_dispatch<EXACT, HAM>(w, group, qrow0, qc, qs, cb, scores + qrow0 * n_tok,
                                HAM ? ham + qrow0 * n_tok : nullptr, n_tok, t);
+}
+
+// ---------------------------------------------------------------------------
+// INT4 on the integer matrix cores, pipelined with the tile DMA (group <= 4).
+//
+// v_mfma_i32_16x16x64_i8: lane L supplies A row / B column L % 16 for the 16
+// K slots 16 (L / 16) .. +15 and receives C[4 (L / 16) + r][L % 16], r < 4.
+//  * Columns are 16 tiles (a "block"; a wave's 64 tiles are 4 blocks).
+//  * Rows are (query j, limb l) = 4 j + l: each query, prescaled by 2^-e
+//    (|q 2^-e| <= 1) and rounded to q30 = q 2^(30 - e), is split into four
+//    signed bytes l0 + 2^8 l1 + 2^16 l2 + 2^24 l3. So lane L's accumulators
+//    are the four limb sums of query L / 16 for its tile.
+//  * B is the nibble n itself (0..15): latent dword x gives the bytes
+//    x & 0x0F0F0F0F (dims 0, 2, 4, 6) and (x >> 4) & 0x0F0F0F0F (dims 1, 3,
+//    5, 7); the staged query bytes use the same K order. K-block kb covers
+//    dims 64 kb .. +63, lane group h the latent dwords 8 kb + 2 h, +1.
+//  * The -8 of n - 8 is exact in integers: the accumulator starts at
+//    -sum_d 8 limb(q_d), one tile-independent product with B = 8 per wave.
+// The limb sums are exact; q is carried to 2^-31 of max |q| (about f32's
+// own rounding). The tile scale applies once per (tile, query); the path serves
+// INT4 tiles whose 8 group scales are equal (every codec-0 tile; eff =
+// scale * gs / 255), other blocks send the wave to the per-codec MFMA paths.
+//
+// Each block's two 1 KiB DMA loads land in its own 2 KiB of the wave's region;
+// the block is scored as soon as they are in (s_waitcnt vmcnt(2 (3 - cb)):
+// loads complete in issue order, so this counts only the later tile loads),
+// while the later blocks are still in flight. The reads of the region are
+// inline asm, invisible to the compiler's LDS-DMA tracking, which would
+// otherwise wait for every tile load before the first read. Scores are stored
+// after the last block: a store before a partial vmcnt wait would make the
+// wait cover it too.
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct I8Staging {
+    uint4 a8[2][4][16];  // A operand [kb][lane group][row]
+    uint32_t qsw[4][8];  // the 4 queries' sign words
+    float qf[4];         // 2^(e - 30) / 255, NaN for a non-finite query
+};
+
+// Tile c of a block: the dwords lane group h reads.
+struct I8BlockWords {
+    uint2 x0, x1;  // latent dwords (2h, 2h+1) and (8+2h, 9+2h)
+    uint4 r0, r1;  // residual words 0..7
+    uint2 m6;      // scale, lambda
+    uint4 m7;      // position, head | flags << 16, gs[0..7]
+};
+
+// LDS byte addresses of tile c's words in block 0 of a wave region filled by
+// fetch_tiles_lds (block cb sits 2048 cb bytes further).
+struct I8BlockAddr {
+    uint32_t x0, x1, r0, r1, m6, m7;
+};
+
+__device__ __forceinline__ I8BlockAddr i8_block_addr(const uint4* region, uint32_t c, uint32_t h) {
+    const uint32_t base = lds_byte_addr(region) + 128u * c, sx = c & 7u;  // tile u = 16 cb + c: u & 7 = c & 7
+    I8BlockAddr a;
+    a.x0 = base + 16u * ((h >> 1) ^ sx) + 8u * (h & 1u);
+    a.x1 = base + 16u * ((2u + (h >> 1)) ^ sx) + 8u * (h & 1u);
+    a.r0 = base + 16u * (4u ^ sx);
+    a.r1 = base + 16u * (5u ^ sx);
+    a.m6 = base + 16u * (6u ^ sx);
+    a.m7 = base + 16u * (7u ^ sx);
+    return a;
+}
+
+// Waits until at most VMCNT tile loads are outstanding, then reads block OFF/2048.
+template <int VMCNT, int OFF>
+__device__ __forceinline__ I8BlockWords i8_read_block(const I8BlockAddr& a) {
+    I8BlockWords b;
+    asm volatile(
+        "s_waitcnt vmcnt(%12)\n\t"
+        "ds_read_b64 %0, %6 offset:%13\n\t"
+        "ds_read_b64 %1, %7 offset:%13\n\t"
+        "ds_read_b128 %2, %8 offset:%13\n\t"
+        "ds_read_b128 %3, %9 offset:%13\n\t"
+        "ds_read_b64 %4, %10 offset:%13\n\t"
+        "ds_read_b128 %5, %11 offset:%13\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(b.x0), "=&v"(b.x1), "=&v"(b.r0), "=&v"(b.r1), "=&v"(b.m6), "=&v"(b.m7)
+        : "v"(a.x0), "v"(a.x1), "v"(a.r0), "v"(a.r1), "v"(a.m6), "v"(a.m7), "n"(VMCNT), "n"(OFF)
+        : "memory");
+    return b;
+}
+
+// The block takes the integer path: INT4 (no codec flag) with equal group scales.
+__device__ __forceinline__ bool i8_block_ok(const I8BlockWords& b) {
+    const uint32_t flags = b.m7.y >> 16;
+    const uint32_t g = b.m7.z;
+    return (flags & kCodecFlags) == 0u && b.m7.w == g && g == (g & 0xFFu) * 0x01010101u;
+}
+
+struct I8Query {
+    v4i a0, a1, neg;  // A per K-block; -8 sum limb(q) per limb row
+    uint32_t qw[8];   // sign words of query h
+    float qf;
+};
+
+__device__ __forceinline__ I8Query i8_load_query(const I8Staging& st, uint32_t c, uint32_t h) {
+    I8Query q;
+    q.a0 = __builtin_bit_cast(v4i, st.a8[0][h][c]);
+    q.a1 = __builtin_bit_cast(v4i, st.a8[1][h][c]);
+    const v4i b8 = v4i{0x08080808, 0x08080808, 0x08080808, 0x08080808};
+    v4i off = __builtin_amdgcn_mfma_i32_16x16x64_i8(q.a0, b8, v4i{0, 0, 0, 0}, 0, 0, 0);
+    off = __builtin_amdgcn_mfma_i32_16x16x64_i8(q.a1, b8, off, 0, 0, 0);
+    q.neg = -off;
+    const uint4 x = *reinterpret_cast<const uint4*>(&st.qsw[h][0]);
+    const uint4 y = *reinterpret_cast<const uint4*>(&st.qsw[h][4]);
+    q.qw[0] = x.x, q.qw[1] = x.y, q.qw[2] = x.z, q.qw[3] = x.w;
+    q.qw[4] = y.x, q.qw[5] = y.y, q.qw[6] = y.z, q.qw[7] = y.w;
+    q.qf = st.qf[h];
+    return q;
+}
+
+// Score of (query h, tile c of the block).
+__device__ __forceinline__ float i8_score_block(const I8BlockWords& b, const I8Query& q) {
+    constexpr uint32_t M = 0x0F0F0F0Fu;
+    const v4i b0 = v4i{(int)(b.x0.x & M), (int)((b.x0.x >> 4) & M), (int)(b.x0.y & M), (int)((b.x0.y >> 4) & M)};
+    const v4i b1 = v4i{(int)(b.x1.x & M), (int)((b.x1.x >> 4) & M), (int)(b.x1.y & M), (int)((b.x1.y >> 4) & M)};
+    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(q.a0, b0, q.neg, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(q.a1, b1, acc, 0, 0, 0);
+    const uint32_t ham = __popc(b.r0.x ^ q.qw[0]) + __popc(b.r0.y ^ q.qw[1]) + __popc(b.r0.z ^ q.qw[2]) +
+                         __popc(b.r0.w ^ q.qw[3]) + __popc(b.r1.x ^ q.qw[4]) + __popc(b.r1.y ^ q.qw[5]) +
+                         __popc(b.r1.z ^ q.qw[6]) + __popc(b.r1.w ^ q.qw[7]);
+    // sum q30 (n - 8) = (acc3 2^8 + acc2) 2^16 + (acc1 2^8 + acc0), both
+    // brackets exact in int32 (|acc| <= 2^17); one rounding each to f32
+    const float dot = fmaf((float)((acc[3] << 8) + acc[2]), 65536.0f, (float)((acc[1] << 8) + acc[0]));
+    const float eff = __uint_as_float(b.m6.x) * (float)(b.m7.z & 0xFFu);
+    float sc = dot * (eff * q.qf);
+    if (((b.m7.y >> 16) & kFlagWarm) == 0u) sc = fmaf(__uint_as_float(b.m6.y), 256.0f - 2.0f * (float)ham, sc);
+    return sc;
+}
+
+// Query staging of the integer path, on top of stage_issue<4> /
+// stage_commit<4>: each wave also loads its query's 8 sign words (lanes 0..7;
+// rows past `group` read as zero) and writes its query's limb bytes, 2^(e-22)
+// and sign words to the I8Staging (inline asm stores, as in stage_f16_row).
+__device__ __forceinline__ uint32_t stage_issue_signs(const uint32_t* __restrict__ qs, size_t qrow0,
+                                                      uint32_t group) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(qs + qrow0 * 8), 0,
+        __builtin_amdgcn_readfirstlane((group < 4u ? group : 4u) * 32u), 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, wv * 32u + 4u * (lane & 7u), 0, 0);
+}
+
+// Bytes l0 | l1 << 8 | l2 << 16 | l3 << 24 of q30 = l0 + 2^8 l1 + 2^16 l2 +
+// 2^24 l3: l0, l1, l2 are the sign-extended low bytes of q30, q1 =
+// (q30 - l0) / 2^8 and q2 = (q1 - l1) / 2^8 (each division exact), so they lie
+// in [-128, 127]; |q30| <= 2^30 gives |q2| <= 2^14 + 1 and l3 = (q2 - l2) /
+// 2^8 in [-64, 64].
+__device__ __forceinline__ uint32_t q30_limbs(int32_t q) {
+    const int32_t q1 = (q - (int32_t)(int8_t)(q & 0xFF)) >> 8;
+    const int32_t q2 = (q1 - (int32_t)(int8_t)(q1 & 0xFF)) >> 8;
+    const int32_t l3 = (q2 - (int32_t)(int8_t)(q2 & 0xFF)) >> 8;
+    return ((uint32_t)q & 0xFFu) | (((uint32_t)q1 & 0xFFu) << 8) | (((uint32_t)q2 & 0xFFu) << 16) |
+           ((uint32_t)l3 << 24);
+}
+
+// Wave j's query: v0 = q_j[d], v1 = q_j[d + 4], d = f16_stage_dim(lane) =
+// 8 p + o (latent dword p = lane / 4, o = lane % 4); sw = sign word lane (< 8).
+__device__ __forceinline__ void stage_i8_row(float v0, float v1, int e, uint32_t sw, uint32_t j,
+                                             I8Staging& st) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t b0 = q30_limbs((int32_t)rintf(ldexpf(v0, 30 - e)));
+    const uint32_t b1 = q30_limbs((int32_t)rintf(ldexpf(v1, 30 - e)));
+    // K slot of dim 8 p + o inside lane group h = (p & 7) / 2 of K-block p / 8:
+    // 8 (p & 1) + 4 (o & 1) + o / 2; dim d + 4 sits two slots further.
+    const uint32_t p = lane >> 2, o = lane & 3u;
+    const uint32_t addr = lds_byte_addr(&st.a8[p >> 3][(p & 7u) >> 1][4u * j]) +
+                          8u * (p & 1u) + 4u * (o & 1u) + (o >> 1);
+    asm volatile(
+        "ds_write_b8 %0, %1\n\tds_write_b8 %0, %2 offset:2\n\t"
+        "ds_write_b8 %0, %3 offset:16\n\tds_write_b8 %0, %4 offset:18\n\t"
+        "ds_write_b8_d16_hi %0, %1 offset:32\n\tds_write_b8_d16_hi %0, %2 offset:34\n\t"
+        "ds_write_b8 %0, %5 offset:48\n\tds_write_b8 %0, %6 offset:50"
+        ::"v"(addr), "v"(b0), "v"(b1), "v"(b0 >> 8), "v"(b1 >> 8), "v"(b0 >> 24), "v"(b1 >> 24)
+        : "memory");
+    // A non-finite query value makes every score of the query NaN (the f16
+    // path propagates it through its products; here the limbs would not).
+    const bool bad = __any(!(fabsf(v0) <= 3.402823466e38f) || !(fabsf(v1) <= 3.402823466e38f));
+    const float qf = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30) * (1.0f / 255.0f);
+    if (lane == 0)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(&st.qf[j])), "v"(qf) : "memory");
+    if (lane < 8)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(&st.qsw[j][lane])), "v"(sw) : "memory");
 }
 
 // Fast scoring of tile rows on the matrix cores (group <= kMfmaMaxGroup).
@@ -740,6 +942,86 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
+// Scoring of rows of INT4 tiles, group <= 4, on the pipelined integer path
+// (the launch takes it when the caller's codec hint is INT4). A wave whose
+// block holds another codec, or group scales that differ, scores its 64
+// tiles on the per-lane path instead: same results, slower. Registers stay
+// within 128 (four waves per SIMD), which a kernel that also carried the
+// per-codec MFMA paths could not do.
+__global__ __launch_bounds__(256, 4) void score_rows_int4_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float cb[16];
+    __shared__ uint4 tile_lds[4][512];  // one 8 KiB region per wave
+    __shared__ I8Staging st;
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // wave w stages query w: its dims (d, d + 4), d = f16_stage_dim(lane), and
+    // its sign words; buffer ranges end at the row's `group` queries
+    float v0, v1;
+    {
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(qc + qrow0 * kDC), 0,
+            __builtin_amdgcn_readfirstlane(group * kDC * 4u), 0x00020000);
+        const uint32_t voff = 4u * f16_stage_dim(lane), soff = wave * kDC * 4u;
+        v0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff, 0, 0));
+        v1 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff + 16u, 0, 0));
+    }
+    const uint32_t sw = stage_issue_signs(qs, qrow0, group);
+    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
+    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+    // keep the staging arithmetic after the tile loads are issued
+    __builtin_amdgcn_sched_barrier(0);
+    stage_codebook(cb);
+    stage_i8_row(v0, v1, stage_exponent(v0, v1), sw, wave, st);
+    lds_barrier();
+    const uint32_t c = lane & 15u, h = lane >> 4;
+    const I8Query q = i8_load_query(st, c, h);
+    const I8BlockAddr a = i8_block_addr(tile_lds[wave], c, h);
+    float res[4];
+    bool ok;
+    {
+        const I8BlockWords b = i8_read_block<6, 0>(a);
+        ok = __all(i8_block_ok(b));
+        if (ok) res[0] = i8_score_block(b, q);
+    }
+    if (ok) {
+        const I8BlockWords b = i8_read_block<4, 2048>(a);
+        ok = __all(i8_block_ok(b));
+        if (ok) res[1] = i8_score_block(b, q);
+    }
+    if (ok) {
+        const I8BlockWords b = i8_read_block<2, 4096>(a);
+        ok = __all(i8_block_ok(b));
+        if (ok) res[2] = i8_score_block(b, q);
+    }
+    if (ok) {
+        const I8BlockWords b = i8_read_block<0, 6144>(a);
+        ok = __all(i8_block_ok(b));
+        if (ok) res[3] = i8_score_block(b, q);
+    }
+    if (ok) {
+        float* out = scores + (qrow0 + h) * n_tok;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t tk = wave0 + 16u * k + c;
+            if (h < group && tk < n_tok) store_out(out + tk, res[k]);
+        }
+        return;
+    }
+    // Per-lane path; nothing was stored above. The compiler waits for the
+    // tile loads before this read-back.
+    uint32_t w[32];
+    fetch_tiles_readback(tile_lds[wave], w);
+    const uint32_t t = wave0 + lane;
+    if (t < n_tok)
+        score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, scores + qrow0 * n_tok, nullptr,
+                                     n_tok, t);
+}
+
 // Wide-group scoring (group > 16, e.g. 64 queries per tile) on
 // v_mfma_f32_16x16x32_f16: rows = queries (blocks of 16), columns = tiles
 // (blocks of 16), K = 32 dims per instruction. Lane L supplies A row / B
@@ -764,7 +1046,6 @@ __device__ __forceinline__ const uint4* tile_chunk(const uint4* region, uint32_t
     return region + 8u * u + (chunk ^ (u & 7u));
 }
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 // +-1 bytes of 8 sign bits: byte j = 1 - 2 * bit j (0x01 or 0xFF).
 __device__ __forceinline__ uint2 pm1_bytes(uint32_t b) {
@@ -976,8 +1257,8 @@ __device__ __forceinline__ void wide_stage_issue(const float* __restrict__ qc,
 #pragma unroll
     for (uint32_t k = 0; k < kWideRowsPerWave; ++k) {
         const uint32_t soff = (wv + 4u * k) * kDC * 4u;
-        r.v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, voff, soff, 0));
-        r.v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, voff + 16u, soff, 0));
+        r.v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff, 0, 0));
+        r.v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff + 16u, 0, 0));
     }
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(qs + qrow0 * 8), 0, __builtin_amdgcn_readfirstlane(group * 32u),
@@ -3478,7 +3759,7 @@ size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, b
 
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
-                             uint32_t* ham, void* workspace, hipStream_t s) {
+                             uint32_t* ham, void* workspace, int codec_hint, hipStream_t s) {
     if (n_rows == 0 || n_tok == 0 || group == 0) return hipSuccess;
     dim3 grid((n_tok + 255) / 256, n_rows);
     const uint4* tp = static_cast<const uint4*>(tiles);
@@ -3486,7 +3767,9 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
         (!exact && !ham && group <= kMfmaMaxGroup) ? staging_bytes(staging_rows(group)) : 0;
     const uint32_t* qsw = reinterpret_cast<const uint32_t*>(qs);
     if (!exact && !ham && group <= kMfmaMaxGroup) {
-        if (group <= 4)
+        if (group <= 4 && codec_hint == kCodecInt4Single)
+            score_rows_int4_kernel<<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
+        else if (group <= 4)
             score_rows_fast_kernel<4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= kRegStageMaxGroup)
             score_rows_fast_kernel<16><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
@@ -3871,7 +4154,7 @@ hipError_t launch_decode_attention(const void* tiles, const void* vals, int v_dt
         attn_combine_kernel<<<dim3(n_rows * group, d_v / 16), 256, 0, s>>>(part, n_seg, group, d_v, scale, out);
         return hipGetLastError();
     }
-    e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr, ws + sb + pb, s);
+    e = launch_score_rows(tiles, n_rows, n_tok, group, qc, qs, false, scores, nullptr, ws + sb + pb, -1, s);
     if (e != hipSuccess) return e;
     const dim3 grid(n_seg, n_rows);
     e = attn_partial_dispatch(grid, scores, vals, v_dtype, n_tok, group, d_v, scale, part, s);

@@ -23,9 +23,12 @@ constexpr uint32_t kTopkMaxCandidates = 8192;
 
 // `workspace`: device memory of score_rows_workspace_bytes() (a staging image
 // per row for 16 < group <= 64 in fast mode; otherwise unused, may be null).
+// `codec_hint`: the codec id the tiles were encoded with, or -1 if unknown;
+// it selects kernels only (kCodecInt4Single: the integer INT4 path for
+// group <= 4) and never changes a result.
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
-                             uint32_t* ham, void* workspace, hipStream_t s);
+                             uint32_t* ham, void* workspace, int codec_hint, hipStream_t s);
 size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham);
 hipError_t launch_score_paged_topk(const void* arena, uint32_t page_shift,
                                   const uint32_t* page_table, uint32_t max_pages,

@@ -288,6 +288,109 @@ def test_score_fast_streaming_ragged(s, torch, group, codec):
         assert_tol(fast[qi, idx], ref)
 
 
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+def test_score_int4_hint_integer_path(s, torch, group):
+    # slha_gpu_score_codec with the INT4 hint: the pipelined integer path
+    # (group <= 4). Ragged rows (n_tok % 64 != 0 and % 16 != 0, waves past the
+    # end), ~30 % WARM tiles, mode R keys; against SCORE_EXACT on every pair
+    # and the oracle on sampled tokens of every row.
+    n_rows, n_tok = 3, 5_003
+    g = torch.Generator(device="cuda").manual_seed(77 + group)
+    keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g).to(torch.bfloat16)
+    r = np.random.default_rng(group)
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    # Tiny and huge queries keep their relative precision: scores of a query
+    # scaled by S are compared after dividing by S, so the tolerance's floor
+    # of 1e-3 sits at the query's own scale (cancellation in a score is
+    # relative to |q| |k|, as in the reference's SIMD-vs-scalar bar).
+    qscale = np.ones(n_rows * group)
+    qscale[0], qscale[-1] = 1e-30, 1e30
+    q = (q * qscale[:, None]).astype(np.float32)
+    if group > 1:
+        # limb edges of the four-byte split of q 2^30 (max |q| = 1 sets the
+        # prescale): values next to multiples of 2^8, 2^16, 2^24 and +-2^30
+        # that f32 holds exactly
+        cand = np.array([k * 2**sh + d for sh in (8, 16, 24) for k in (-64, -3, -1, 1, 2, 63)
+                         for d in (-129, -128, -127, -1, 1, 127, 128)]
+                        + [2**30, -(2**30), 2**30 - 128, -(2**30) + 128], np.float64)
+        cand = cand[(np.abs(cand) <= 2**30) & (cand.astype(np.float32) == cand)]
+        qe = np.resize(cand, 128)
+        qe[1::2] = -qe[1::2]
+        q[1] = (qe / 2**30).astype(np.float32)
+        q[1, 0] = 1.0
+    with s.Model(seed=5 + group) as m:
+        td = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE, n_kv_heads=n_rows)
+        warm = np.flatnonzero(r.random(n_rows * n_tok) < 0.3).astype(np.int32)
+        s.gpu_ccos_apply(td, dev(torch, warm), 0)
+        qc, qs = s.gpu_prepare_queries(m, dev(torch, q))
+    hinted = s.gpu_score(td, qc, qs, group=group, codec_hint=s.CODEC_INT4_SINGLE).cpu().numpy()
+    plain = s.gpu_score(td, qc, qs, group=group).cpu().numpy()
+    exact = s.gpu_score(td, qc, qs, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+    qsc = qscale[:, None]
+    assert_tol(hinted / qsc, exact / qsc)
+    assert_tol(plain / qsc, exact / qsc)
+    tn = tiles_np(td)
+    qn, qsn = qc.cpu().numpy(), qs.cpu().numpy().view(np.uint64)
+    idx = np.r_[0:80, 2_000:2_064, n_tok - 80:n_tok]
+    for row in range(n_rows):
+        for j in range(group):
+            qi = row * group + j
+            ref, _ = o.score(tn[row * n_tok + idx], qn[qi], qsn[qi])
+            assert np.array_equal(exact[qi, idx].view(np.uint32), ref.view(np.uint32))
+            assert_tol(hinted[qi, idx] / qscale[qi], ref / qscale[qi])
+
+
+@pytest.mark.parametrize("case", ["mx_int4", "mixed_codecs", "one_nf4_tile", "one_tile_gs", "nan_query"])
+def test_score_int4_hint_fallback(s, torch, case):
+    # The INT4 hint on tiles that do not all fit the integer path: a wave with
+    # any such tile in any of its four 16-tile blocks scores on the per-lane
+    # path; results match SCORE_EXACT either way. A NaN query value gives NaN
+    # scores for that query, as on the other paths.
+    n_rows, n_tok, group = 2, 4_100, 4
+    r = np.random.default_rng(hash(case) % 1000)
+    if case == "mixed_codecs":
+        td = dev(torch, random_tiles(n_rows * n_tok, 11).view(np.uint8).reshape(n_rows, n_tok, 128))
+    else:
+        g = torch.Generator(device="cuda").manual_seed(3)
+        keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
+        codec = s.CODEC_INT4_GROUPED if case == "mx_int4" else s.CODEC_INT4_SINGLE
+        with s.Model(seed=9) as m:
+            td = s.gpu_encode(m, keys, codec, n_kv_heads=n_rows)
+        tn = td.cpu().numpy().reshape(-1, 128).copy()
+        if case == "one_nf4_tile":  # tile 50 of wave 1 (block 3) is NF4
+            tn[64 + 50, 118] |= 2
+        if case == "one_tile_gs":  # tile 20 of wave 2 (block 1): unequal group scales
+            tn[128 + 20, 121] = 200
+        td = dev(torch, tn.reshape(n_rows, n_tok, 128))
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    if case == "nan_query":
+        q[5, 77] = np.nan
+    qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
+    qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
+    hinted = s.gpu_score(td, qd, qsd, group=group, codec_hint=s.CODEC_INT4_SINGLE).cpu().numpy()
+    exact = s.gpu_score(td, qd, qsd, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+    if case == "nan_query":
+        assert np.isnan(hinted[5]).all() and np.isnan(exact[5]).all()
+        keep = np.ones(n_rows * group, bool)
+        keep[5] = False
+        hinted, exact = hinted[keep], exact[keep]
+    assert np.isfinite(hinted).all()
+    assert_tol(hinted, exact)
+
+
+def test_score_codec_hint_rejects_unknown(s, torch):
+    tiles = torch.zeros((1, 64, 128), dtype=torch.uint8, device="cuda")
+    qc = torch.zeros((1, 128), dtype=torch.float32, device="cuda")
+    qs = torch.zeros((1, 4), dtype=torch.int64, device="cuda")
+    out = torch.empty((1, 64), dtype=torch.float32, device="cuda")
+    vp = s.ctypes.c_void_p
+    for bad in (-2, 6):
+        rc = s.lib.slha_gpu_score_codec(vp(tiles.data_ptr()), 1, 64, vp(qc.data_ptr()),
+                                        vp(qs.data_ptr()), 1, s.SCORE_FAST, bad,
+                                        vp(out.data_ptr()), None, None)
+        assert rc == s.ERR_CODEC
+
+
 def test_score_fast_wide_group_c4_shape(s, torch):
     # C4 shape: one row, 64 queries per tile (TQ3 + RHT tiles).
     keys = keys_for(99, 2048, "scaled")
@@ -452,10 +555,13 @@ def test_c2_full_size_properties(s, torch):
         tiles = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE, n_kv_heads=8)
         qc, qs = s.gpu_prepare_queries(m, q)
         fast = s.gpu_score(tiles, qc, qs, group=4)
+        hinted = s.gpu_score(tiles, qc, qs, group=4, codec_hint=s.CODEC_INT4_SINGLE)
         exact, ham = s.gpu_score(tiles, qc, qs, group=4, mode=s.SCORE_EXACT, hamming=True)
     fast, exact, ham = fast.cpu().numpy(), exact.cpu().numpy(), ham.cpu().numpy()
+    hinted = hinted.cpu().numpy()
     assert fast.shape == (32, 32768)
     assert_tol(fast, exact)
+    assert_tol(hinted, exact)
     # sampled oracle checks: tile bytes, Hamming, exact scores
     kn = keys.float().cpu().numpy()
     tn = tiles.cpu().numpy().reshape(8, 32768, 128)
