@@ -16,6 +16,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libslha.so"
+# bench.py's floor kernel (not part of the product library)
+BENCH_LIB = PKG / "libslha_bench.so"
 ORACLE = ROOT / "oracle"
 ORACLE_LIB = ORACLE / "liboracle_slha.so"
 CPU_BASELINE_LIB = ORACLE / "libcpu_baseline.so"
@@ -66,6 +68,14 @@ def build_library(verbose: bool = True) -> Path:
     return LIB
 
 
+def build_bench_library() -> Path:
+    tmp = BENCH_LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *HIPCC_FLAGS, str(CSRC / "bench_floor.hip"), "-o", str(tmp)]
+    _run(cmd, CSRC)
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
+
+
 def build_oracle() -> Path:
     cc = shutil.which("gcc") or "cc"
     common = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
@@ -82,6 +92,7 @@ def build_oracle() -> Path:
 def build_all() -> None:
     build_oracle()
     build_library()
+    build_bench_library()
 
 
 if __name__ == "__main__":
@@ -90,5 +101,7 @@ if __name__ == "__main__":
         build_oracle()
     elif what == "lib":
         build_library()
+    elif what == "bench":
+        build_bench_library()
     else:
         build_all()

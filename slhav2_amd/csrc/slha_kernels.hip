@@ -17,6 +17,7 @@
 //   observe_*_kernel       CCOS H2O importance from the arena's scores (ccos.rs:257-300)
 #include "slha_device.h"
 #include "slha_launch.h"
+#include "slha_tile_io.h"
 
 #include <algorithm>
 #include <climits>
@@ -180,15 +181,6 @@ __device__ __forceinline__ void decode_group_exact(const uint32_t* w, int g, con
 // group at a time for one query at a time; the empty asm makes the tile words
 // opaque per query so the compiler cannot hoist all 128 decoded values out of
 // the query loop (which would cost 128 VGPRs and most of the occupancy).
-// Scores and Hamming distances are written once and not read again by the
-// scoring kernels: non-temporal stores stream them out of L2 as they are
-// written instead of leaving 4 B per pair dirty there. At the C2 size
-// (4 MiB of scores per launch) this took the launch from ~9.5 to ~8.9 us.
-template <typename T>
-__device__ __forceinline__ void store_out(T* p, T v) {
-    __builtin_nontemporal_store(v, p);
-}
-
 template <int CLS, bool EXACT, bool HAM>
 __device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group, size_t qrow0,
                                            const float* __restrict__ qc,
@@ -253,10 +245,6 @@ __device__ __forceinline__ void score_lane(const uint32_t* w_in, uint32_t group,
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// LDS byte address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 constexpr uint32_t kQStride = 132;      // LDS row stride of a staged query (floats)
 constexpr uint32_t kQStrideH = 264;     // u16 words per staged f16 query (512 B + 16 B pad)
@@ -553,12 +541,9 @@ __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t
 // (m = 0 -> e = 0); v0, v1 are this lane's two values.
 __device__ __forceinline__ int stage_exponent(float v0, float v1) {
     const float m = wave_max_nonneg(fmaxf(fabsf(v0), fabsf(v1)));
-    int e = 0;
-    if (m > 0.0f) {
-        (void)frexpf(m, &e);
-        if (ldexpf(1.0f, e - 1) == m) e -= 1;
-    }
-    return e;
+    // m = 2^e' * mant, mant in [0.5, 1); a power of two (mant = 0.5) is its
+    // own bound. Zero gives exponent 0 and mantissa 0.
+    return __builtin_amdgcn_frexp_exp(m) - (__builtin_amdgcn_frexp_mant(m) == 0.5f ? 1 : 0);
 }
 
 // v0 = q_j[d], v1 = q_j[d + 4] with d = f16_stage_dim(lane); one wave per query.
@@ -626,6 +611,11 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ void stage_codebook(float* cb) {
     if (threadIdx.x < 16) cb[threadIdx.x] = nf4_level(threadIdx.x);
 }
+// The same by the first 16 lanes of the calling wave.
+__device__ __forceinline__ void stage_codebook_wave(float* cb) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (lane < 16) cb[lane] = nf4_level(lane);
+}
 
 template <bool EXACT, bool HAM>
 __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group, size_t qrow0,
@@ -643,51 +633,6 @@ __device__ __forceinline__ void score_dispatch(const uint32_t* w, uint32_t group
 #undef SLHA_LANE
 }
 
-// Coalesced direct-to-LDS fetch of a wave's 64 consecutive tiles (8 KiB)
-// into its LDS region. buffer_load_dwordx4 ... lds writes lane l of load j to
-// region + 1024 j + 16 l; each lane picks the global chunk that belongs in
-// that slot under the swizzle "chunk c of tile u at uint4 slot
-// 8u + (c ^ (u & 7))", so every load instruction reads 1 KiB of contiguous
-// HBM (8 lanes per 128-B tile, chunks permuted inside the tile) and no VGPRs
-// hold the data in flight. The buffer's range ends at the last valid tile:
-// slots of tiles at or past n_valid read as zero. The compiler waits for
-// these loads (vmcnt) before the region is read back.
-// Cache policy of the tile loads: nt (streaming). A launch reads each tile
-// once; at C2 this took the launch from ~8.9 to ~8.7 us.
-constexpr int kCachePolicyNT = 2;
-
-__device__ __forceinline__ void fetch_tiles_lds(const uint4* wave_base, uint32_t n_valid,
-                                                uint4* region) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t in_tile = (lane & 0x38u) + ((lane & 7u) ^ (lane >> 3));
-    // readfirstlane: the range is wave-uniform, and a descriptor built from
-    // VGPRs would be legalised into a loop over lanes.
-    const uint32_t bytes = __builtin_amdgcn_readfirstlane((n_valid < 64u ? n_valid : 64u) * 128u);
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(wave_base), 0, bytes, 0x00020000);
-    // The whole offset in the VGPR operand: the range check of a raw buffer
-    // load covers it but not the SGPR offset.
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rsrc, (__attribute__((address_space(3))) void*)(region + 64 * j), 16,
-            1024u * j + in_tile * 16u, 0, 0, kCachePolicyNT);
-}
-
-// Lane l reads tile l back from a region filled by fetch_tiles_lds; the XOR
-// swizzle keeps these reads free of bank conflicts. Only lanes of one wave
-// touch the region, so no barrier is needed.
-__device__ __forceinline__ void fetch_tiles_readback(const uint4* region, uint32_t* w) {
-    const uint32_t lane = threadIdx.x & 63u;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const uint4 x = region[8u * lane + (c ^ (lane & 7u))];
-        w[4 * c + 0] = x.x;
-        w[4 * c + 1] = x.y;
-        w[4 * c + 2] = x.z;
-        w[4 * c + 3] = x.w;
-    }
-}
 
 // Per-lane scoring of tile rows: EXACT mode, Hamming output, or groups too
 // large for the staged MFMA path.
@@ -731,6 +676,9 @@ __global__ __launch_bounds__(256) void score_rows_kernel(
 // INT4 tiles whose 8 group scales are equal (every codec-0 tile; eff =
 // scale * gs / 255), other blocks send the wave to the per-codec MFMA paths.
 //
+// The wave's tiles are dealt into four blocks (block k holds tiles 4c + k,
+// fetch_tiles_lds_dealt), so after the last block a lane holds four
+// consecutive tokens and stores them as one 16-byte write.
 // Each block's two 1 KiB DMA loads land in its own 2 KiB of the wave's region;
 // the block is scored as soon as they are in (s_waitcnt vmcnt(2 (3 - cb)):
 // loads complete in issue order, so this counts only the later tile loads),
@@ -763,7 +711,7 @@ struct I8BlockAddr {
 };
 
 __device__ __forceinline__ I8BlockAddr i8_block_addr(const uint4* region, uint32_t c, uint32_t h) {
-    const uint32_t base = lds_byte_addr(region) + 128u * c, sx = c & 7u;  // tile u = 16 cb + c: u & 7 = c & 7
+    const uint32_t base = lds_byte_addr(region) + 128u * c, sx = c & 7u;  // local tile c, swizzled by c & 7
     I8BlockAddr a;
     a.x0 = base + 16u * ((h >> 1) ^ sx) + 8u * (h & 1u);
     a.x1 = base + 16u * ((2u + (h >> 1)) ^ sx) + 8u * (h & 1u);
@@ -795,9 +743,9 @@ __device__ __forceinline__ I8BlockWords i8_read_block(const I8BlockAddr& a) {
 
 // The block takes the integer path: INT4 (no codec flag) with equal group scales.
 __device__ __forceinline__ bool i8_block_ok(const I8BlockWords& b) {
-    const uint32_t flags = b.m7.y >> 16;
-    const uint32_t g = b.m7.z;
-    return (flags & kCodecFlags) == 0u && b.m7.w == g && g == (g & 0xFFu) * 0x01010101u;
+    const uint32_t g = b.m7.z;  // all 8 bytes equal: the word equals its byte rotation and m7.w
+    return ((b.m7.y >> 16) & kCodecFlags) == 0u && b.m7.w == g &&
+           __builtin_amdgcn_alignbit(g, g, 8) == g;
 }
 
 struct I8Query {
@@ -836,9 +784,10 @@ __device__ __forceinline__ float i8_score_block(const I8BlockWords& b, const I8Q
     // brackets exact in int32 (|acc| <= 2^17); one rounding each to f32
     const float dot = fmaf((float)((acc[3] << 8) + acc[2]), 65536.0f, (float)((acc[1] << 8) + acc[0]));
     const float eff = __uint_as_float(b.m6.x) * (float)(b.m7.z & 0xFFu);
-    float sc = dot * (eff * q.qf);
-    if (((b.m7.y >> 16) & kFlagWarm) == 0u) sc = fmaf(__uint_as_float(b.m6.y), 256.0f - 2.0f * (float)ham, sc);
-    return sc;
+    const float sc = dot * (eff * q.qf);
+    // the residual term always, then a select: no branch around it
+    const float with_res = fmaf(__uint_as_float(b.m6.y), 256.0f - 2.0f * (float)ham, sc);
+    return ((b.m7.y >> 16) & kFlagWarm) == 0u ? with_res : sc;
 }
 
 // Query staging of the integer path, on top of stage_issue<4> /
@@ -891,10 +840,10 @@ __device__ __forceinline__ void stage_i8_row(float v0, float v1, int e, uint32_t
     // path propagates it through its products; here the limbs would not).
     const bool bad = __any(!(fabsf(v0) <= 3.402823466e38f) || !(fabsf(v1) <= 3.402823466e38f));
     const float qf = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30) * (1.0f / 255.0f);
-    if (lane == 0)
-        asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(&st.qf[j])), "v"(qf) : "memory");
-    if (lane < 8)
-        asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(&st.qsw[j][lane])), "v"(sw) : "memory");
+    // every lane writes (lanes l and l + 8 hold the same sign word): no branch
+    asm volatile("ds_write_b32 %0, %1\n\tds_write_b32 %2, %3" ::"v"(lds_byte_addr(&st.qf[j])),
+                 "v"(qf), "v"(lds_byte_addr(&st.qsw[j][lane & 7u])), "v"(sw)
+                 : "memory");
 }
 
 // Fast scoring of tile rows on the matrix cores (group <= kMfmaMaxGroup).
@@ -972,50 +921,68 @@ __global__ __launch_bounds__(256, 4) void score_rows_int4_kernel(
     const uint32_t sw = stage_issue_signs(qs, qrow0, group);
     const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
-    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+    fetch_tiles_lds_dealt(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
     // keep the staging arithmetic after the tile loads are issued
     __builtin_amdgcn_sched_barrier(0);
-    stage_codebook(cb);
     stage_i8_row(v0, v1, stage_exponent(v0, v1), sw, wave, st);
     lds_barrier();
     const uint32_t c = lane & 15u, h = lane >> 4;
     const I8Query q = i8_load_query(st, c, h);
     const I8BlockAddr a = i8_block_addr(tile_lds[wave], c, h);
+    // This lane's outputs: query h, tokens wave0 + 4c .. +3 (block k holds
+    // token 4c + k), computed while the tiles are in flight.
+    const size_t o = (qrow0 + h) * n_tok + wave0 + 4u * c;
+    // wave-uniform: every lane stores all four, 16-byte aligned
+    const bool whole = group == 4u && wave0 + 64u <= n_tok && (n_tok & 3u) == 0u &&
+                       (reinterpret_cast<uintptr_t>(scores) & 15u) == 0u;
+    // Every block is scored as it lands; whether the wave's tiles all fit the
+    // integer path is decided once, after the last block (a block that does
+    // not fit only yields values that are then discarded). The empty asm pins
+    // each block's score where it is computed: sunk to the stores, four
+    // blocks' accumulators would be live at once.
     float res[4];
     bool ok;
     {
         const I8BlockWords b = i8_read_block<6, 0>(a);
-        ok = __all(i8_block_ok(b));
-        if (ok) res[0] = i8_score_block(b, q);
+        ok = i8_block_ok(b);
+        res[0] = i8_score_block(b, q);
+        asm volatile("" : "+v"(res[0]));
     }
-    if (ok) {
+    {
         const I8BlockWords b = i8_read_block<4, 2048>(a);
-        ok = __all(i8_block_ok(b));
-        if (ok) res[1] = i8_score_block(b, q);
+        ok = ok & i8_block_ok(b);
+        res[1] = i8_score_block(b, q);
+        asm volatile("" : "+v"(res[1]));
     }
-    if (ok) {
+    {
         const I8BlockWords b = i8_read_block<2, 4096>(a);
-        ok = __all(i8_block_ok(b));
-        if (ok) res[2] = i8_score_block(b, q);
+        ok = ok & i8_block_ok(b);
+        res[2] = i8_score_block(b, q);
+        asm volatile("" : "+v"(res[2]));
     }
-    if (ok) {
+    {
         const I8BlockWords b = i8_read_block<0, 6144>(a);
-        ok = __all(i8_block_ok(b));
-        if (ok) res[3] = i8_score_block(b, q);
+        ok = ok & i8_block_ok(b);
+        res[3] = i8_score_block(b, q);
     }
-    if (ok) {
-        float* out = scores + (qrow0 + h) * n_tok;
+    if (__all(ok)) {
+        if (whole) {  // 16 lanes x 16 B: 256 contiguous bytes per query
+            typedef float v4f_nt __attribute__((ext_vector_type(4)));
+            __builtin_nontemporal_store(v4f_nt{res[0], res[1], res[2], res[3]},
+                                        reinterpret_cast<v4f_nt*>(scores + o));
+        } else {
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-            const uint32_t tk = wave0 + 16u * k + c;
-            if (h < group && tk < n_tok) store_out(out + tk, res[k]);
+            for (uint32_t k = 0; k < 4; ++k)
+                if (h < group && wave0 + 4u * c + k < n_tok) store_out(scores + o + k, res[k]);
         }
         return;
     }
     // Per-lane path; nothing was stored above. The compiler waits for the
-    // tile loads before this read-back.
+    // tile loads before this read-back. The wave stages the NF4 codebook for
+    // itself (waves that reach here write identical values; no barrier).
+    stage_codebook_wave(cb);
     uint32_t w[32];
-    fetch_tiles_readback(tile_lds[wave], w);
+    fetch_tiles_readback_dealt(tile_lds[wave], w);
     const uint32_t t = wave0 + lane;
     if (t < n_tok)
         score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, scores + qrow0 * n_tok, nullptr,

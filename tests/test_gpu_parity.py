@@ -378,6 +378,25 @@ def test_score_int4_hint_fallback(s, torch, case):
     assert_tol(hinted, exact)
 
 
+def test_score_int4_hint_unaligned_output(s, torch):
+    # Output rows that are not 16-byte aligned (scores buffer at an offset of
+    # one float; n_tok a multiple of 4 and not) take the per-element stores.
+    n_rows, group = 2, 4
+    for n_tok in (4_096, 4_098):
+        g = torch.Generator(device="cuda").manual_seed(n_tok)
+        keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
+        q = torch.randn((n_rows * group, 128), device="cuda", generator=g)
+        with s.Model(seed=2) as m:
+            td = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE, n_kv_heads=n_rows)
+            qc, qs = s.gpu_prepare_queries(m, q)
+        buf = torch.full((n_rows * group * n_tok + 1,), -7.0, dtype=torch.float32, device="cuda")
+        view = buf[1:].view(n_rows * group, n_tok)
+        s.gpu_score(td, qc, qs, group=group, codec_hint=s.CODEC_INT4_SINGLE, out=view)
+        exact = s.gpu_score(td, qc, qs, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+        assert buf[0].item() == -7.0
+        assert_tol(view.cpu().numpy(), exact)
+
+
 def test_score_codec_hint_rejects_unknown(s, torch):
     tiles = torch.zeros((1, 64, 128), dtype=torch.uint8, device="cuda")
     qc = torch.zeros((1, 128), dtype=torch.float32, device="cuda")
