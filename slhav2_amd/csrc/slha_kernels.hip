@@ -819,9 +819,14 @@ __device__ __forceinline__ uint32_t q30_limbs(int32_t q) {
 
 // Wave j's query: v0 = q_j[d], v1 = q_j[d + 4], d = f16_stage_dim(lane) =
 // 8 p + o (latent dword p = lane / 4, o = lane % 4); sw = sign word lane (< 8).
-__device__ __forceinline__ void stage_i8_row(float v0, float v1, int e, uint32_t sw, uint32_t j,
+__device__ __forceinline__ void stage_i8_row(float v0, float v1, uint32_t sw, uint32_t j,
                                              I8Staging& st) {
     const uint32_t lane = threadIdx.x & 63u;
+    // max |q| over the wave as an integer max of the bit patterns, in which
+    // NaN sorts above +inf above every finite value; e as in stage_exponent
+    const float m = wave_max_nonneg(__uint_as_float(
+        max(__float_as_uint(fabsf(v0)), __float_as_uint(fabsf(v1)))));
+    const int e = __builtin_amdgcn_frexp_exp(m) - (__builtin_amdgcn_frexp_mant(m) == 0.5f ? 1 : 0);
     const uint32_t b0 = q30_limbs((int32_t)rintf(ldexpf(v0, 30 - e)));
     const uint32_t b1 = q30_limbs((int32_t)rintf(ldexpf(v1, 30 - e)));
     // K slot of dim 8 p + o inside lane group h = (p & 7) / 2 of K-block p / 8:
@@ -838,8 +843,7 @@ __device__ __forceinline__ void stage_i8_row(float v0, float v1, int e, uint32_t
         : "memory");
     // A non-finite query value makes every score of the query NaN (the f16
     // path propagates it through its products; here the limbs would not).
-    const bool bad = __any(!(fabsf(v0) <= 3.402823466e38f) || !(fabsf(v1) <= 3.402823466e38f));
-    const float qf = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30) * (1.0f / 255.0f);
+    const float qf = m <= 3.402823466e38f ? ldexpf(1.0f, e - 30) * (1.0f / 255.0f) : __builtin_nanf("");
     // every lane writes (lanes l and l + 8 hold the same sign word): no branch
     asm volatile("ds_write_b32 %0, %1\n\tds_write_b32 %2, %3" ::"v"(lds_byte_addr(&st.qf[j])),
                  "v"(qf), "v"(lds_byte_addr(&st.qsw[j][lane & 7u])), "v"(sw)
@@ -924,7 +928,7 @@ __global__ __launch_bounds__(256, 4) void score_rows_int4_kernel(
     fetch_tiles_lds_dealt(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
     // keep the staging arithmetic after the tile loads are issued
     __builtin_amdgcn_sched_barrier(0);
-    stage_i8_row(v0, v1, stage_exponent(v0, v1), sw, wave, st);
+    stage_i8_row(v0, v1, sw, wave, st);
     lds_barrier();
     const uint32_t c = lane & 15u, h = lane >> 4;
     const I8Query q = i8_load_query(st, c, h);
