@@ -144,9 +144,27 @@ def cpu_encode_baseline(keys_f32, z, gpu_tiles, threads: int) -> dict:
             "sample": f"{n} C2 keys (head 0, tokens 0..{n - 1}), INT4 mode R; tiles equal the GPU's"}
 
 
-def cpu_baseline(tiles_np, qc_np, qs_np, threads: int) -> dict:
-    """Time the reference's CPU compute_score dispatch (restated in C) on a
-    bounded sample: whole C2 steps, repeated; median of 5 after a warm-up."""
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the affinity mask, bounded by the
+    process's CPU share where the host states one (OMP_NUM_THREADS; the GPU
+    boxes give one GPU's process a 16-CPU share and export 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
+
+
+def cpu_rows_baseline(tiles_np, qc_np, qs_np, group: int, sample: str, gpu_scores=None) -> dict:
+    """Pairs scored per second by the reference's CPU compute_score dispatch
+    (oracle/cpu_baseline.c: AVX-512 / AVX2 kernels of every codec, VPOPCNTDQ
+    Hamming) over tiles_np [rows, n_tok, 128] and group queries per row; median
+    of 5 after a warm-up, all threads of cpu_threads(), plus one thread.
+    gpu_scores (same layout) is compared with the CPU's scores: both are held
+    to 1e-3 (1 + |s|) of the exact path, so they agree within 2e-3."""
     import numpy as np
 
     lib = ctypes.CDLL(str(ROOT / "oracle" / "libcpu_baseline.so"))
@@ -154,12 +172,18 @@ def cpu_baseline(tiles_np, qc_np, qs_np, threads: int) -> dict:
                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                                    ctypes.c_void_p, ctypes.c_int]
     lib.cpu_baseline_isa.restype = ctypes.c_int
-    out = np.empty((N_Q, N_TOK), np.float32)
+    lib.cpu_baseline_vpopcntdq.restype = ctypes.c_int
+    tiles_np = np.ascontiguousarray(tiles_np)
+    qc_np, qs_np = np.ascontiguousarray(qc_np, np.float32), np.ascontiguousarray(qs_np)
+    rows, n_tok = tiles_np.shape[0], tiles_np.shape[1]
+    pairs = rows * group * n_tok
+    out = np.empty((rows * group, n_tok), np.float32)
+    threads = cpu_threads()
 
     def run(nthreads: int) -> float:
         t0 = time.perf_counter()
-        lib.cpu_score_rows(tiles_np.ctypes.data, N_KV, N_TOK, qc_np.ctypes.data,
-                           qs_np.ctypes.data, GROUP, out.ctypes.data, nthreads)
+        lib.cpu_score_rows(tiles_np.ctypes.data, rows, n_tok, qc_np.ctypes.data,
+                           qs_np.ctypes.data, group, out.ctypes.data, nthreads)
         return time.perf_counter() - t0
 
     run(threads)  # warm-up
@@ -169,14 +193,22 @@ def cpu_baseline(tiles_np, qc_np, qs_np, threads: int) -> dict:
         times.append(sum(run(threads) for _ in range(reps)) / reps)
     t1 = run(1)
     isa = {2: "avx512f", 1: "avx2", 0: "scalar"}[lib.cpu_baseline_isa()]
-    return {
-        "value": PAIRS / statistics.median(times),
+    pop = "vpopcntdq" if lib.cpu_baseline_vpopcntdq() else "popcnt"
+    res = {
+        "value": pairs / statistics.median(times),
         "unit": "tiles/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"full C2 step ({PAIRS} pairs) x {reps} reps, median of 5; "
-                  f"single-thread {PAIRS / t1:.3e} tiles/s; isa {isa}; cpu {cpu_model()}",
+        "sample": f"{sample} ({pairs} pairs) x {reps} reps, median of 5; single-thread "
+                  f"{pairs / t1:.3e} tiles/s; isa {isa}, hamming {pop}; cpu {cpu_model()}",
     }
+    if gpu_scores is not None:
+        g = np.asarray(gpu_scores, np.float64).reshape(out.shape)
+        rel = float(np.max(np.abs(out - g) / (1.0 + np.abs(g))))
+        if not rel <= 2e-3:
+            raise RuntimeError(f"CPU baseline disagrees with the GPU on its sample: {rel}")
+        res["max_rel_diff_vs_gpu"] = rel
+    return res
 
 
 def timed_steps(step, steps: int, warmup: int, stream) -> float:
@@ -266,21 +298,32 @@ def run_c3(args) -> int:
     results = {}
     with s.Model(seed=0x5EED0004, rht=False, residual_mode=s.RESIDUAL_R) as m:
         qc, qs = s.gpu_prepare_queries(m, q)
+        exact = torch.empty_like(scores)
         for name, codec in (("nf4", s.CODEC_NF4), ("mx_int4", s.CODEC_INT4_GROUPED)):
             enc_ms = timed_once(lambda: s.gpu_encode(m, keys, codec, n_kv_heads=n_kv, out=tiles,
                                                      stream=stream), stream)
-            score = s.lib.slha_gpu_score
+            score = s.lib.slha_gpu_score_codec
             vp = ctypes.c_void_p
             a = (vp(tiles.data_ptr()), rows, n_tok, vp(qc.data_ptr()), vp(qs.data_ptr()), GROUP,
-                 s.SCORE_FAST, vp(scores.data_ptr()), None, vp(stream.cuda_stream))
+                 s.SCORE_FAST, codec, vp(scores.data_ptr()), None, vp(stream.cuda_stream))
             ms = timed_steps(lambda i: score(*a), steps, warmup, stream)
-            ex = s.gpu_score(tiles[:1], qc[:GROUP], qs[:GROUP], group=GROUP, mode=s.SCORE_EXACT)
-            err = ((scores[:GROUP] - ex).abs() / (1 + ex.abs())).max().item()
+            # every pair of the step against the reference-order exact path
+            s.gpu_score(tiles, qc, qs, group=GROUP, mode=s.SCORE_EXACT, out=exact, stream=stream)
+            err = ((scores - exact).abs() / (1 + exact.abs())).max().item()
+            if not err <= 1e-3:
+                raise RuntimeError(f"C3 {name}: fast scores differ from the exact path ({err})")
             results[name] = {"ms_per_step": ms, "tiles_per_s": n_q * n_tok / (ms * 1e-3),
                              "roofline": hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<4u>", f"c3_{name}"),
                              "encode_keys_per_s": rows * n_tok / (enc_ms * 1e-3),
-                             "encode_ms": enc_ms, "fast_vs_exact_max_rel_err_row0": err}
+                             "encode_ms": enc_ms, "fast_vs_exact_max_rel_err_all_pairs": err}
+            if not args.no_cpu_baseline:
+                # sequence 0 (8 KV heads x 131 072 tokens, its 32 query heads)
+                results[name]["cpu_baseline"] = cpu_rows_baseline(
+                    tiles[:n_kv].cpu().numpy(), qc[:n_kv * GROUP].cpu().numpy(),
+                    qs[:n_kv * GROUP].cpu().numpy(), GROUP, f"C3 {name}, sequence 0",
+                    gpu_scores=scores[:n_kv * GROUP].cpu().numpy())
     best = results["mx_int4"]
+    extra = {"cpu_baseline": best["cpu_baseline"]} if "cpu_baseline" in best else {}
     print(json.dumps(line(
         "tiles scored/s + HBM GB/s % of peak; keys encoded/s", best["tiles_per_s"], "tiles/s",
         steps, warmup, best["ms_per_step"], "f32",
@@ -288,7 +331,7 @@ def run_c3(args) -> int:
          "sequences": n_seq, "kv_heads": n_kv, "tokens_per_head": n_tok, "query_heads": n_q,
          "group": GROUP, "codecs": "nf4, mx_int4 (run separately; value = mx_int4)",
          "parallelism": "none (1 GPU)"},
-        per_codec=results)), flush=True)
+        per_codec=results, **extra)), flush=True)
     return 0
 
 
@@ -319,6 +362,13 @@ def run_c4(args) -> int:
         ms = timed_steps(lambda i: score(*a), steps, warmup, stream)
         ex = s.gpu_score(tiles[:, :4096], qc, qs, group=n_q, mode=s.SCORE_EXACT)
         err = ((scores[:, :4096] - ex).abs() / (1 + ex.abs())).max().item()
+        extra = {}
+        if not args.no_cpu_baseline:
+            n_cpu = 1 << 16  # the first 65 536 tiles against all 64 queries
+            extra["cpu_baseline"] = cpu_rows_baseline(
+                tiles[:, :n_cpu].cpu().numpy(), qc.cpu().numpy(), qs.cpu().numpy(), n_q,
+                f"C4, tiles 0..{n_cpu - 1} x 64 queries",
+                gpu_scores=scores[:, :n_cpu].cpu().numpy())
     nbytes = n_keys * TILE_BYTES + n_q * n_keys * 4 + n_q * (D * 4 + 32)
     flops = n_q * n_keys * 2 * D
     enc_bytes = n_keys * (D * 2 + TILE_BYTES)
@@ -331,7 +381,7 @@ def run_c4(args) -> int:
         score_tflops=flops / (ms * 1e-3) / 1e12, fast_vs_exact_max_rel_err_first4096=err,
         encode={"keys_per_s": n_keys / (enc_ms * 1e-3), "ms": enc_ms,
                 "hbm_gbs": enc_bytes / (enc_ms * 1e-3) / 1e9,
-                **encode_mfma(n_keys / (enc_ms * 1e-3))})), flush=True)
+                **encode_mfma(n_keys / (enc_ms * 1e-3))}, **extra)), flush=True)
     return 0
 
 
@@ -444,6 +494,22 @@ def run_c5(args) -> int:
     a0 = a[:13] + (0,) + a[14:]
     ms_score = timed_steps(lambda i: fn(*a0), steps, warmup, stream)
     n_warm = int(len(warm))
+    extra = {}
+    if not args.no_cpu_baseline:
+        # sequence 0's tiles gathered back out of the arena through the page
+        # table (WARM tiles included), scored on the CPU against its 32 queries
+        L0 = lens[0]
+        rows0 = torch.empty((n_kv, L0, 128), dtype=torch.uint8, device="cuda")
+        for h in range(n_kv):
+            for pg in range(-(-L0 // page)):
+                phys = int(table[0, h, pg])
+                n = min(page, L0 - pg * page)
+                rows0[h, pg * page: pg * page + n] = arena[phys * page: phys * page + n]
+        torch.cuda.synchronize()
+        extra["cpu_baseline"] = cpu_rows_baseline(
+            rows0.cpu().numpy(), qc[:hq].cpu().numpy(), qs[:hq].cpu().numpy(), GROUP,
+            f"C5 sequence 0 ({L0} tokens, 8 KV heads)",
+            gpu_scores=scores[:hq * L0].view(hq, L0).cpu().numpy())
     logical_tile_bytes = (total_tiles - n_warm) * 128 + n_warm * 96
     nbytes = (logical_tile_bytes + pairs * 4 + n_seq * hq * k * 8 + n_seq * hq * (D * 4 + 32)
               + table.numel() * 4)
@@ -456,7 +522,8 @@ def run_c5(args) -> int:
          "parallelism": "none (1 GPU)"},
         roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_segment_kernel + topk_merge_kernel", "c5"),
         score_only_ms=ms_score, topk_ms=ms - ms_score,
-        score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9)), flush=True)
+        score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9, **extra)),
+        flush=True)
     return 0
 
 
@@ -774,13 +841,10 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        try:
-            threads = len(os.sched_getaffinity(0))
-        except AttributeError:
-            threads = os.cpu_count() or 1
-        threads = max(1, min(threads, 16))
-        result["cpu_baseline"] = cpu_baseline(sets[0].cpu().numpy(), qc.cpu().numpy(),
-                                              qs.cpu().numpy(), threads)
+        threads = cpu_threads()
+        result["cpu_baseline"] = cpu_rows_baseline(sets[0].cpu().numpy(), qc.cpu().numpy(),
+                                                   qs.cpu().numpy(), GROUP, "full C2 step",
+                                                   gpu_scores=ref.cpu().numpy())
         # keys encoded/s on the CPU: the first 32768 keys of head 0 of the
         # encode-timing key set, compared with the GPU's tiles of those keys
         z, _ = model.projection()
