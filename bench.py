@@ -662,6 +662,72 @@ def run_learned(args) -> int:
     return 0
 
 
+def run_hostpath(args) -> int:
+    """Latency of the host-pointer C ABI (slha.h, what the llama.cpp shim
+    calls): slha_score_tiles over n = 1, 4 096 and 2^20 tiles in pageable host
+    memory (each call validates the tiles, copies them and the query to the
+    device, scores, copies the scores back and synchronises), and
+    slha_process_tile, slha_prepare_query and slha_encode_key for one key or
+    query. Median of the timed calls, wall clock."""
+    import numpy as np
+    import torch
+
+    import slhav2_amd as s
+
+    res = {}
+    with s.Model(seed=0x5EED000A, rht=False, residual_mode=s.RESIDUAL_R) as m:
+        g = torch.Generator(device="cuda").manual_seed(0x5EED000B)
+        keys = torch.randn((1, 1 << 20, D), device="cuda", generator=g).to(torch.bfloat16)
+        tiles = s.gpu_encode(m, keys, s.CODEC_INT4_SINGLE).reshape(-1, 128).cpu().numpy()
+        q = np.random.default_rng(1).normal(size=D).astype(np.float32)
+        qc = np.zeros(D, np.float32)
+        qs = np.zeros(4, np.uint64)
+        s.lib.slha_prepare_query(m.handle, q.ctypes.data, D, qc.ctypes.data, qs.ctypes.data)
+
+        def median_us(fn, reps):
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                rc = fn()
+                ts.append(time.perf_counter() - t0)
+                if rc != 0:
+                    raise RuntimeError(f"host ABI call failed: {rc} {s.last_error()}")
+            return statistics.median(ts) * 1e6
+
+        for n in (1, 4096, 1 << 20):
+            out = np.empty(n, np.float32)
+            t = np.ascontiguousarray(tiles[:n])
+            us = median_us(lambda: s.lib.slha_score_tiles(m.handle, t.ctypes.data, n, qc.ctypes.data,
+                                                          qs.ctypes.data, out.ctypes.data),
+                           50 if n < (1 << 20) else 10)
+            res[f"slha_score_tiles_n{n}"] = {"us_per_call": us, "tiles_per_s": n / (us * 1e-6),
+                                             "host_bytes_per_s": n * (TILE_BYTES + 4) / (us * 1e-6)}
+        one = np.empty(1, np.float32)
+        t1 = np.ascontiguousarray(tiles[:1])
+        res["slha_process_tile"] = {"us_per_call": median_us(
+            lambda: s.lib.slha_process_tile(t1.ctypes.data, qc.ctypes.data, qs.ctypes.data,
+                                            one.ctypes.data), 50)}
+        qc2, qs2 = np.zeros(D, np.float32), np.zeros(4, np.uint64)
+        res["slha_prepare_query"] = {"us_per_call": median_us(
+            lambda: s.lib.slha_prepare_query(m.handle, q.ctypes.data, D, qc2.ctypes.data,
+                                             qs2.ctypes.data), 50)}
+        key = np.random.default_rng(2).normal(size=D).astype(np.float32)
+        tile = np.zeros(128, np.uint8)
+        res["slha_encode_key"] = {"us_per_call": median_us(
+            lambda: s.lib.slha_encode_key(m.handle, key.ctypes.data, D, 0, s.CODEC_INT4_SINGLE,
+                                          tile.ctypes.data), 50)}
+    n = 1 << 20
+    big = res[f"slha_score_tiles_n{n}"]
+    print(json.dumps(line(
+        "host-pointer C ABI: tiles scored/s (slha_score_tiles, 2^20 tiles)", big["tiles_per_s"],
+        "tiles/s", 10, 1, big["us_per_call"] / 1000.0, "f32",
+        {"workload": "slha.h host entry points, pageable host buffers, INT4 tiles",
+         "parallelism": "none (1 GPU)"},
+        latency=res)), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -672,7 +738,7 @@ def main() -> int:
                     help="GQA group of --config decode (default 4, the C2 shape; 1..16)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to calibrate HBM byte counters")
-    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos", "learned"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5", "decode", "evict", "ccos", "learned", "hostpath"], default="c2",
                     help="c2 (default) is the headline; c3/c4/c5 measure the other "
                          "BASELINE configs at full size")
     args = ap.parse_args()
@@ -686,7 +752,8 @@ def main() -> int:
         return copy_calibration()
     if args.config != "c2":
         return {"c3": run_c3, "c4": run_c4, "c5": run_c5, "decode": run_decode,
-                "evict": run_evict, "ccos": run_ccos, "learned": run_learned}[args.config](args)
+                "evict": run_evict, "ccos": run_ccos, "learned": run_learned,
+                "hostpath": run_hostpath}[args.config](args)
 
     import torch
 

@@ -74,11 +74,14 @@ def _load() -> ctypes.CDLL:
         import torch  # noqa: F401
     except ImportError:
         pass
-    if not LIB_PATH.exists():
+    # SLHA_LIBRARY names another build of the same library (for example the
+    # host-sanitizer build, slhav2_amd/build.py sanitize); default libslha.so.
+    path = Path(os.environ.get("SLHA_LIBRARY", "") or LIB_PATH)
+    if not path.exists():
         raise ImportError(
-            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
+            f"{path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`"
         )
-    return ctypes.CDLL(str(LIB_PATH))
+    return ctypes.CDLL(str(path))
 
 
 lib = _load()

@@ -68,6 +68,31 @@ def build_library(verbose: bool = True) -> Path:
     return LIB
 
 
+# Host-side sanitizer build of the product library (CPU tests only; the GPU
+# code is compiled as usual): AddressSanitizer and UndefinedBehaviorSanitizer
+# on the host C++ - the .slhw loader, the EventLog file side, the CCOS host
+# mirror and every argument check. tests/run_sanitized.sh runs the CPU tests
+# against it.
+ASAN_LIB = PKG / "libslha_asan.so"
+SANITIZE_HOST = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-shared-libasan",
+]
+
+
+def build_sanitized_library() -> Path:
+    srcs = [str(CSRC / s) for s in HIP_SOURCES]
+    tmp = ASAN_LIB.with_suffix(".so.tmp")
+    flags = [f for f in HIPCC_FLAGS if f != "-O3"] + ["-O1", "-g"]
+    cmd = [_hipcc(), *flags, *SANITIZE_HOST, "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
+    _run(cmd, CSRC)
+    os.replace(tmp, ASAN_LIB)
+    return ASAN_LIB
+
+
 def build_bench_library() -> Path:
     tmp = BENCH_LIB.with_suffix(".so.tmp")
     cmd = [_hipcc(), *HIPCC_FLAGS, str(CSRC / "bench_floor.hip"), "-o", str(tmp)]
@@ -103,5 +128,7 @@ if __name__ == "__main__":
         build_library()
     elif what == "bench":
         build_bench_library()
+    elif what == "sanitize":
+        build_sanitized_library()
     else:
         build_all()
