@@ -63,15 +63,26 @@ extern "C" {
 #define SLHA_FLAG_TQ3_NOCORR (1u << 4)
 #define SLHA_FLAG_MIX3 (1u << 5)
 
-/* slha.h:53-57 — this build always uses 64-byte tile alignment. */
+/*
+ * slha.h:48-57 — tile alignment. 64 bytes by default. Define
+ * SLHA_CACHE_LINE_128=1 when linking against a build of this library made
+ * with the same definition (SLHA_CACHE_LINE_128=1 in the environment of
+ * slhav2_amd/build.py), whose slha_tile_align() returns 128. The byte layout
+ * and the 128-byte size are the same either way; only the alignment the
+ * compiler assumes for a tile changes.
+ */
+#if defined(SLHA_CACHE_LINE_128) && SLHA_CACHE_LINE_128
+#define SLHA_TILE_ALIGN 128u
+#else
 #define SLHA_TILE_ALIGN 64u
+#endif
 
 /*
  * slha.h:87-98 — the 128-byte tile (tile.rs:52-77). Byte map: latent 0..64,
  * residual 64..96 (4 little-endian u64), scale 96, lambda 100, sigma 104,
  * token_id 108, position 112, head_id 116, flags 118, group_scales 120..128.
  */
-typedef struct __attribute__((aligned(64))) {
+typedef struct __attribute__((aligned(SLHA_TILE_ALIGN))) {
     uint8_t latent_kv[SLHA_LATENT_BYTES];
     uint64_t residual_bitmap[SLHA_RESIDUAL_WORDS];
     float scale;
@@ -100,6 +111,7 @@ static_assert(alignof(SciRustSlhaTile) == SLHA_TILE_ALIGN, "tile alignment");
 _Static_assert(sizeof(SciRustSlhaTile) == 128u, "tile is 128 bytes");
 _Static_assert(offsetof(SciRustSlhaTile, flags) == 118u, "flags offset");
 _Static_assert(offsetof(SciRustSlhaTile, group_scales) == 120u, "group_scales offset");
+_Static_assert(_Alignof(SciRustSlhaTile) == SLHA_TILE_ALIGN, "tile alignment");
 #endif
 
 typedef struct SlhaContext SlhaContext;

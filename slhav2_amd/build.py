@@ -59,10 +59,17 @@ def _run(cmd: list[str], cwd: Path) -> None:
     subprocess.run(cmd, cwd=cwd, check=True)
 
 
+def _layout_defines() -> list[str]:
+    # SLHA_CACHE_LINE_128=1: 128-byte tile alignment (include/slha.h); callers
+    # then compile against the header with the same definition.
+    v = os.environ.get("SLHA_CACHE_LINE_128", "")
+    return ["-DSLHA_CACHE_LINE_128=1"] if v not in ("", "0") else []
+
+
 def build_library(verbose: bool = True) -> Path:
     srcs = [str(CSRC / s) for s in HIP_SOURCES]
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *_layout_defines(), "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
     _run(cmd, CSRC)
     os.replace(tmp, LIB)
     return LIB
@@ -87,7 +94,8 @@ def build_sanitized_library() -> Path:
     srcs = [str(CSRC / s) for s in HIP_SOURCES]
     tmp = ASAN_LIB.with_suffix(".so.tmp")
     flags = [f for f in HIPCC_FLAGS if f != "-O3"] + ["-O1", "-g"]
-    cmd = [_hipcc(), *flags, *SANITIZE_HOST, "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
+    cmd = [_hipcc(), *flags, *SANITIZE_HOST, *_layout_defines(), "-I", str(ROOT / "include"), *srcs,
+           "-o", str(tmp)]
     _run(cmd, CSRC)
     os.replace(tmp, ASAN_LIB)
     return ASAN_LIB

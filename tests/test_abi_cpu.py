@@ -57,6 +57,34 @@ def test_layout_and_versions():
     assert s.TILE_DTYPE.fields["group_scales"][1] == 120
 
 
+@pytest.mark.parametrize("lang", ["c", "c++"])
+@pytest.mark.parametrize("line128", [False, True])
+def test_header_alignment_option(tmp_path, lang, line128):
+    # slha.h:48-57 and tests.rs:12-20: SLHA_CACHE_LINE_128=1 gives 128-byte
+    # alignment, otherwise 64; the tile is 128 bytes with no padding and the
+    # same field offsets either way (the header's static asserts hold).
+    src = tmp_path / ("t.c" if lang == "c" else "t.cpp")
+    src.write_text("""#include <stdio.h>
+#include "slha.h"
+int main(void) {
+    SciRustSlhaTile a[3];
+    printf("%u %zu %zu %zu\\n", SLHA_TILE_ALIGN, sizeof(SciRustSlhaTile),
+           (size_t)((char*)&a[1] - (char*)&a[0]), (size_t)offsetof(SciRustSlhaTile, group_scales));
+    return (int)((unsigned long long)(size_t)a % SLHA_TILE_ALIGN);
+}
+""")
+    exe = tmp_path / "t"
+    cc = "gcc" if lang == "c" else "g++"
+    std = "-std=c11" if lang == "c" else "-std=c++17"
+    cmd = [cc, std, "-Wall", "-Werror", "-I", str(ROOT / "include"), str(src), "-o", str(exe)]
+    if line128:
+        cmd.insert(1, "-DSLHA_CACHE_LINE_128=1")
+    subprocess.run(cmd, check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0
+    assert r.stdout.split() == [str(128 if line128 else 64), "128", "128", "120"]
+
+
 def test_null_pointer_errors_leave_outputs_untouched():
     out = np.full(1, 42.0, np.float32)
     rc = s.lib.slha_process_tile(None, None, None, out.ctypes.data)
