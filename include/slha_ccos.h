@@ -13,8 +13,12 @@
  * accumulated there from the scores of the whole arena.
  *
  * Calls are synchronous on `stream` (they return after their device work is
- * done), as the reference's methods are. One cache is not safe for concurrent
- * calls from several threads.
+ * done), as the reference's methods are, except slha_ccos_observe_scores,
+ * which only enqueues its kernels: it is called once per decode step, and
+ * what it changes (the device importance) is read back only by later calls,
+ * which order themselves after it on their stream. Use one stream per cache,
+ * or order the streams yourself. One cache is not safe for concurrent calls
+ * from several threads.
  */
 #ifndef SLHA_CCOS_H
 #define SLHA_CCOS_H
@@ -79,7 +83,9 @@ int32_t slha_ccos_insert(SlhaCcos* c, const SciRustSlhaTile* tiles_dev, size_t n
  * tiles). COLD slots are skipped; a non-finite live score, a non-finite or
  * non-positive temperature, or no live slot leaves importance unchanged.
  * Importance[s] += softmax((score - max) / temperature)[s] in f32; the sum is
- * a tree sum, so the result is within a few ulps of the reference's. */
+ * a tree sum, so the result is within a few ulps of the reference's.
+ * Returns once the kernels are enqueued on `stream` (no synchronisation);
+ * scores_dev must stay valid until they run. */
 int32_t slha_ccos_observe_scores(SlhaCcos* c, const float* scores_dev, size_t n, float temperature,
                                  void* stream);
 

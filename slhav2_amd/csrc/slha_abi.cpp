@@ -1824,9 +1824,11 @@ int32_t slha_ccos_observe_scores(SlhaCcos* c, const float* scores_dev, size_t n,
         if (n == 0 || !std::isfinite(temperature) || temperature <= 0.0f) return;
         if (!scores_dev) fail(SLHA_ERR_NULL, "slha_ccos_observe_scores received a NULL pointer");
         const hipStream_t s = static_cast<hipStream_t>(stream);
+        // Stream-ordered, no synchronisation: importance and the workspace
+        // stay on the device, and every later call that reads them (evict
+        // ordering, slha_ccos_slots) copies them on its stream and waits.
         check_hip(launch_observe_scores(scores_dev, C->state_dev, n, temperature, C->importance, C->obs_ws, s),
                   "observe kernels");
-        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
     });
 }
 

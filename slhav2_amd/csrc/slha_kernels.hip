@@ -993,30 +993,34 @@ __global__ __launch_bounds__(256, 4) void score_rows_int4_kernel(
                                      n_tok, t);
 }
 
-// Wide-group scoring (group > 16, e.g. 64 queries per tile) on
-// v_mfma_f32_16x16x32_f16: rows = queries (blocks of 16), columns = tiles
-// (blocks of 16), K = 32 dims per instruction. Lane L supplies A row / B
-// column L % 16 for the 8 consecutive K slots 8 (L / 16) .. +7, and holds
-// C[4 (L / 16) + r][L % 16]. K is permuted so that lane group h = L / 16
-// covers latent dword 4h + ks at K-step ks (dims 8 (4h + ks) .. +7), in the
-// (d0, d4, d1, d5 | d2, d6, d3, d7) order of the staged f16 queries.
-//  * INT4: B = (n - 8) * gs in f16, exact (|.| <= 2040).
-//  * TQ3: level * 4 = 4 code + 2 corr - 15 (NOCORR: 4 code - 14) is an
-//    integer in [-15, 15]; with gs = 16 gs_hi + gs_lo, B_lo = L * gs_lo and
-//    B_hi = L * 16 gs_hi are exact in f16 and go through separate MFMAs.
-// Each B is decoded once per (tile block, K-step) and used by every query
-// block; queries are f16 hi + lo as on the INT4 path.
+// Wide-group scoring (16 < group <= 64 queries per tile, e.g. 64) on the
+// 32x32 matrix-core shapes: v_mfma_f32_32x32x16_f16 for the codes and
+// v_mfma_i32_32x32x32_i8 for the residual term. Rows (A) are queries,
+// columns (B) are tiles: lane L holds, for its tile L % 32, the scores of
+// queries 8 (i / 4) + 4 (L / 32) + i % 4 in accumulator i, so one register
+// store writes two queries' scores for 32 consecutive tiles (whole 128-byte
+// lines).
+//
+// K order, the same on both operands: at f16 K-step ks (16 dims) lane group
+// g = L / 32 supplies K slots 8 g .. 8 g + 7, which are dims
+// 64 g + 8 ks + (s >> 1) + 4 (s & 1), s = 0..7. B's dword k then holds dims
+// (k, k + 4) of an 8-dim window as f16 (lo, hi), which both codecs' bit
+// layouts give with one shift and one masked OR per dword; the f16 value is
+// a magic-number float (exponent bits OR'd over the field) minus its base.
+// Each level enters B exactly:
+//  * INT4: (n - 8) * gs, |.| <= 2040, exact in f16.
+//  * TQ3: L = 4 code + 2 corr - 15 (NOCORR: 4 code - 14), and L * gs
+//    (|.| <= 3825) is split into B_main = f16(L * gs) and its exact rounding
+//    error B_err = L * gs - B_main (-1, 0 or 1). The sum is B_main * q_hi +
+//    B_main * q_lo + B_err * q_hi; the dropped B_err * q_lo is below 2^-22 of
+//    the product.
+// Queries enter as f16 hi + lo of q * 2^-e (e: the query's power-of-two
+// normalisation, undone in the epilogue), exact to ~2^-22 per element.
+// The residual term takes +-1 bytes of both sign sketches on the i8 MFMA:
+// their dot product is 256 - 2 * Hamming, exactly.
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ v8h as_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    return __builtin_bit_cast(v8h, make_uint4(a, b, c, d));
-}
-
-// Tile u's 16-B chunk `chunk` in a wave region filled by fetch_tiles_lds.
-__device__ __forceinline__ const uint4* tile_chunk(const uint4* region, uint32_t u, uint32_t chunk) {
-    return region + 8u * u + (chunk ^ (u & 7u));
-}
-
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 // +-1 bytes of 8 sign bits: byte j = 1 - 2 * bit j (0x01 or 0xFF).
 __device__ __forceinline__ uint2 pm1_bytes(uint32_t b) {
@@ -1026,330 +1030,372 @@ __device__ __forceinline__ uint2 pm1_bytes(uint32_t b) {
     return make_uint2(spread(b & 15u), spread((b >> 4) & 15u));
 }
 
-// 16 sign bits as an i8 MFMA operand of +-1 bytes (bit j -> byte j), from
-// the 256-entry byte table.
-__device__ __forceinline__ v4i pm1_operand(uint32_t bits16, const uint2* lut) {
-    const uint2 a = lut[bits16 & 0xFFu], b = lut[(bits16 >> 8) & 0xFFu];
-    return v4i{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
+// The wide query image of one row: wide_nq(group) query rows (rows at or
+// past `group` are zero), laid out so that every LDS read of the scoring
+// kernel is 16 bytes per lane at consecutive addresses:
+//   H [ks 0..7][part: 0 hi, 1 lo][g 0..1][q]: 8 f16, the K slots above
+//   P [kc 0..7][g][q]: 16 bytes 1 - 2 bit for sign bits 128 g + 16 kc + j
+//   E [q]: 2^e
+__host__ __device__ constexpr uint32_t wide_nq(uint32_t group) { return group <= 32u ? 32u : 64u; }
+__host__ __device__ constexpr uint32_t wide_off_p(uint32_t nq) { return 512u * nq; }
+__host__ __device__ constexpr uint32_t wide_off_e(uint32_t nq) { return 768u * nq; }
+__host__ __device__ constexpr size_t wide_image_bytes(uint32_t group) {
+    return ((size_t)wide_nq(group) * 772u + 1023u) & ~(size_t)1023u;
 }
 
-template <int CLS>
-__device__ __forceinline__ void score_wave_wide(const uint4* region, uint32_t group,
-                                                const uint16_t* qh, const float* qexp,
-                                                const uint32_t* qsl, const uint2* lut,
-                                                float* __restrict__ out, uint32_t n_tok,
-                                                uint32_t tile0) {
-    const uint32_t lane = threadIdx.x & 63u, c = lane & 15u, h = lane >> 4;
-    const uint32_t nrb = (group + 15u) >> 4;  // 2..4 query blocks
-    uint32_t lat[4][4], gsw[4][2];
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const uint32_t u = 16u * cb + c;
-        if constexpr (CLS == kClsInt4) {
-            const uint4 x = *tile_chunk(region, u, h);
-            lat[cb][0] = x.x, lat[cb][1] = x.y, lat[cb][2] = x.z, lat[cb][3] = x.w;
-        } else {  // TQ3: code dwords 3h .. 3h+2, correction dword 12 + h
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t d = i < 3 ? 3u * h + i : 12u + h;
-                lat[cb][i] = reinterpret_cast<const uint32_t*>(tile_chunk(region, u, d >> 2))[d & 3u];
-            }
-        }
-        const uint2 g = reinterpret_cast<const uint2*>(tile_chunk(region, u, 7))[1];
-        gsw[cb][0] = g.x, gsw[cb][1] = g.y;
-    }
-    const uint32_t flags0 = reinterpret_cast<const uint32_t*>(tile_chunk(region, 0, 7))[1] >> 16;
-    const bool nocorr = (flags0 & kFlagNoCorr) != 0;  // uniform: the wave is one codec
-    uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));
-    const v2h k_lo = v2h{(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const v2h k_sixteenth = v2h{(_Float16)0.0625f, (_Float16)0.0625f};
-    const v2h k_hi = v2h{(_Float16)-72.0f, (_Float16)-72.0f};
-    const _Float16 tq_off = nocorr ? (_Float16)-1038.0f : (_Float16)-1039.0f;  // 1024 + 14 / 15
-    const v2h k_tq = v2h{tq_off, tq_off};
-    v4f acc[4][4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const uint32_t p = 4u * h + ks;  // latent dword (8 dims) this lane covers
-        v8h ahi[4], alo[4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const uint32_t row = 16u * rb + c;
-            const bool ok = row < group;
-            const uint16_t* qa = qh + (ok ? row : 0u) * kQStrideH + 16u * p;
-            uint4 x = *reinterpret_cast<const uint4*>(qa);
-            uint4 y = *reinterpret_cast<const uint4*>(qa + 8);
-            if (!ok) x = y = make_uint4(0u, 0u, 0u, 0u);
-            ahi[rb] = __builtin_bit_cast(v8h, x);
-            alo[rb] = __builtin_bit_cast(v8h, y);
-        }
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            const uint32_t gi = 2u * h + (ks >> 1);  // group of dword p
-            const uint32_t gs = (gsw[cb][gi >> 2] >> (8u * (gi & 3u))) & 0xFFu;
-            if constexpr (CLS == kClsInt4) {
-                const _Float16 gh = (_Float16)(float)gs;
-                const v2h g2 = v2h{gh, gh};
-                const uint32_t x = lat[cb][ks], x8 = x >> 8;
-                const v2h l0 = (as_v2h((x & 0x000F000Fu) | magic) + k_lo) * g2;
-                const v2h l1 = __builtin_elementwise_fma(as_v2h((x & 0x00F000F0u) | magic),
-                                                         k_sixteenth, k_hi) * g2;
-                const v2h l2 = (as_v2h((x8 & 0x000F000Fu) | magic) + k_lo) * g2;
-                const v2h l3 = __builtin_elementwise_fma(as_v2h((x8 & 0x00F000F0u) | magic),
-                                                         k_sixteenth, k_hi) * g2;
-                const v8h b = as_v8h(__builtin_bit_cast(uint32_t, l0), __builtin_bit_cast(uint32_t, l1),
-                                     __builtin_bit_cast(uint32_t, l2), __builtin_bit_cast(uint32_t, l3));
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    if ((uint32_t)rb < nrb) {
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], b, acc[rb][cb], 0, 0, 0);
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], b, acc[rb][cb], 0, 0, 0);
-                    }
-                }
-            } else {
-                // 24 code bits of dims 8p .. 8p+7 (bit 3i = dim 8p+i) from the
-                // lane's 96 code bits, and their 8 correction bits
-                const uint32_t x = ks == 0 ? lat[cb][0]
-                                 : ks == 1 ? __builtin_amdgcn_alignbit(lat[cb][1], lat[cb][0], 24)
-                                 : ks == 2 ? __builtin_amdgcn_alignbit(lat[cb][2], lat[cb][1], 16)
-                                           : lat[cb][2] >> 8;
-                const uint32_t cr = nocorr ? 0u : (lat[cb][3] >> (8 * ks)) & 0xFFu;
-                uint32_t pr[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // (dim i, dim i + 4): 4 code + 2 corr in the low / high half
-                    const uint32_t v0 = (((x >> (3 * i)) & 7u) << 2) | (((cr >> i) & 1u) << 1);
-                    const uint32_t v1 = (((x >> (3 * i + 12)) & 7u) << 2) | (((cr >> (i + 4)) & 1u) << 1);
-                    pr[i] = __builtin_bit_cast(uint32_t, as_v2h((v0 | (v1 << 16)) | magic) + k_tq);
-                }
-                const _Float16 glo = (_Float16)(float)(gs & 15u);
-                const _Float16 ghi = (_Float16)(float)(gs & 0xF0u);
-                const v2h g_lo = v2h{glo, glo}, g_hi = v2h{ghi, ghi};
-                const v8h blo = as_v8h(
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[0]) * g_lo),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[1]) * g_lo),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[2]) * g_lo),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[3]) * g_lo));
-                const v8h bhi = as_v8h(
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[0]) * g_hi),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[1]) * g_hi),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[2]) * g_hi),
-                    __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, pr[3]) * g_hi));
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    if ((uint32_t)rb < nrb) {
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], blo, acc[rb][cb], 0, 0, 0);
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], blo, acc[rb][cb], 0, 0, 0);
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rb], bhi, acc[rb][cb], 0, 0, 0);
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rb], bhi, acc[rb][cb], 0, 0, 0);
-                    }
-                }
-            }
-        }
-    }
-    // Residual term on i8 MFMA: with +-1 bytes x = 1 - 2 bit, the dot product
-    // of a query's and a tile's 256 sign bits is 256 - 2 * Hamming, exactly.
-    // The i8 MFMA's K = 64 slots of lane group h are bits 64 kc + 16 h ..
-    // +15 on both operands. A (queries, rows q = 16 rb + L % 16) is expanded
-    // once per wave; B (tiles) once per tile block.
-    v4i aq[4][4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        const uint32_t q = 16u * rb + c;
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            const uint32_t w = (uint32_t)rb < nrb && q < group ? qsl[8u * q + 2u * kc + (h >> 1)] : 0u;
-            aq[rb][kc] = pm1_operand(w >> (16u * (h & 1u)), lut);
-        }
-    }
-    // Epilogue: lane L owns tiles u = 16 cb + L % 16 and queries q = 16 rb + 4h + r.
-    const float lvl = CLS == kClsInt4 ? 1.0f : 0.25f;  // TQ3 levels were scaled by 4
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const uint32_t u = 16u * cb + c;
-        const uint32_t t = tile0 + u;
-        const uint4 m6 = *tile_chunk(region, u, 6);
-        const uint4 m7 = *tile_chunk(region, u, 7);
-        const uint4 r0 = *tile_chunk(region, u, 4);
-        const uint4 r1 = *tile_chunk(region, u, 5);
-        const float s255 = __uint_as_float(m6.x) * (1.0f / 255.0f) * lvl;
-        const float lambda = __uint_as_float(m6.y);
-        const bool warm = ((m7.y >> 16) & kFlagWarm) != 0;
-        const bool odd = (h >> 1) != 0;  // word 2 kc + (h >> 1) of the residual
-        const uint32_t sh = 16u * (h & 1u);
-        v4i bt[4];
-        bt[0] = pm1_operand((odd ? r0.y : r0.x) >> sh, lut);
-        bt[1] = pm1_operand((odd ? r0.w : r0.z) >> sh, lut);
-        bt[2] = pm1_operand((odd ? r1.y : r1.x) >> sh, lut);
-        bt[3] = pm1_operand((odd ? r1.w : r1.z) >> sh, lut);
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            if ((uint32_t)rb >= nrb) continue;
-            v4i dot = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc)
-                dot = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq[rb][kc], bt[kc], dot, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t q = 16u * rb + 4u * h + r;
-                if (q >= group) continue;
-                float sc = acc[rb][cb][r] * (s255 * qexp[q]);
-                if (!warm) sc = fmaf(lambda, (float)dot[r], sc);  // (float)(256 - 2 ham)
-                if (t < n_tok) store_out(out + (size_t)q * n_tok + t, sc);
-            }
-        }
-    }
-}
-
-// Query staging of score_rows_wide_kernel in two phases, as stage_issue /
-// stage_commit: the loads of the row's queries (wave wv takes rows wv + 4k)
-// and sign words go out before the tile DMA, so waiting for them does not
-// wait for the tiles; the conversion and LDS stores come after. Buffer loads
-// past `group` rows read zero.
-constexpr uint32_t kWideRowsPerWave = kMfmaMaxGroup / 4;
-struct WideQueryRegs {
-    float v0[kWideRowsPerWave], v1[kWideRowsPerWave];
-    uint32_t sw[kMfmaMaxGroup * 8 / 256];
-};
-
-__device__ __forceinline__ void wide_stage_issue(const float* __restrict__ qc,
-                                                 const uint32_t* __restrict__ qs, size_t qrow0,
-                                                 uint32_t group, WideQueryRegs& r) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// The row's wide query image, built in LDS by the workgroup: wave w stages
+// queries w, w + 8, ... . Lane l converts dims (d, d + 4),
+// d = 8 (l / 4) + l % 4 = 64 g + 8 ks + k, which are K slots (2k, 2k + 1)
+// of step ks for lane group g: dword k of the 16-byte entry. Buffer loads
+// over exactly the row's `group` queries read zero past them, so the rows
+// of the last query block past `group` are zero.
+template <uint32_t NQB>
+__device__ __forceinline__ void wide_stage_lds(const float* __restrict__ qc,
+                                               const uint32_t* __restrict__ qs, size_t qrow0,
+                                               uint32_t group, char* img) {
+    constexpr uint32_t NQ = 32u * NQB, PER = NQ / 8u;
+    const uint32_t lane = threadIdx.x & 63u, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t d = f16_stage_dim(lane);
+    const uint32_t g = lane >> 5, ks = (lane >> 2) & 7u, k = lane & 3u;
+    // P: chunk c = lane / 4 (kc = c & 7, gp = c >> 3), dword k = sign bits
+    // 128 gp + 16 kc + 4 k .. + 3
+    const uint32_t kc = (lane >> 2) & 7u, gp = lane >> 5;
+    const uint32_t bit = 128u * gp + 16u * kc + 4u * k;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(qc + qrow0 * kDC), 0, __builtin_amdgcn_readfirstlane(group * kDC * 4u),
         0x00020000);
-    const uint32_t voff = 4u * f16_stage_dim(lane);
-#pragma unroll
-    for (uint32_t k = 0; k < kWideRowsPerWave; ++k) {
-        const uint32_t soff = (wv + 4u * k) * kDC * 4u;
-        r.v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff, 0, 0));
-        r.v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, soff + voff + 16u, 0, 0));
-    }
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(qs + qrow0 * 8), 0, __builtin_amdgcn_readfirstlane(group * 32u),
-        0x00020000);
+        const_cast<uint32_t*>(qs + qrow0 * 8), 0, __builtin_amdgcn_readfirstlane(group * 32u), 0x00020000);
+    float v0[PER], v1[PER];
+    uint32_t sw[PER];
 #pragma unroll
-    for (uint32_t k = 0; k < kMfmaMaxGroup * 8 / 256; ++k)
-        r.sw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (threadIdx.x + 256u * k), 0, 0);
+    for (uint32_t i = 0; i < PER; ++i) {  // all loads first, then the conversions
+        const uint32_t j = wv + 8u * i;
+        v0[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, (j * kDC + d) * 4u, 0, 0));
+        v1[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, (j * kDC + d + 4u) * 4u, 0, 0));
+        sw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (j * 8u + (bit >> 5)) * 4u, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < PER; ++i) {
+        const uint32_t j = wv + 8u * i;
+        const int e = stage_exponent(v0[i], v1[i]);
+        const float inv = ldexpf(1.0f, -e);
+        const float d0 = v0[i] * inv, d1 = v1[i] * inv;
+        // Truncating f16 split: x - hi is exact in f32 and lo keeps 11 more bits.
+        const auto hi = __builtin_amdgcn_cvt_pkrtz(d0, d1);
+        const auto lo = __builtin_amdgcn_cvt_pkrtz(d0 - (float)hi.x, d1 - (float)hi.y);
+        const uint32_t h_hi = (((ks * 2u + 0u) * 2u + g) * NQ + j) * 16u + 4u * k;
+        const uint32_t h_lo = (((ks * 2u + 1u) * 2u + g) * NQ + j) * 16u + 4u * k;
+        *reinterpret_cast<uint32_t*>(img + h_hi) = __builtin_bit_cast(uint32_t, hi);
+        *reinterpret_cast<uint32_t*>(img + h_lo) = __builtin_bit_cast(uint32_t, lo);
+        const uint32_t pm = j < group ? pm1_bytes((sw[i] >> (bit & 31u)) & 15u).x : 0u;
+        *reinterpret_cast<uint32_t*>(img + wide_off_p(NQ) + ((kc * 2u + gp) * NQ + j) * 16u + 4u * k) = pm;
+        if (lane == 0) *reinterpret_cast<float*>(img + wide_off_e(NQ) + 4u * j) = ldexpf(1.0f, e);
+    }
 }
 
-__device__ __forceinline__ void wide_stage_commit(const WideQueryRegs& r, uint32_t group,
-                                                  uint16_t* q16, float* qexp, uint32_t* qsl) {
-    const uint32_t wv = threadIdx.x >> 6;
-    const uint32_t rows = (group + 3u) & ~3u;
+// A lane's share of one tile (its tile L % 32 of a 32-tile block, half
+// g = L / 32): the 64-byte latent, 16 residual bytes (bits 128 g .. +127),
+// scale and lambda, the flags word and its group-scale dword (groups
+// 4 g .. 4 g + 3). Loaded before the block's codec is known; the codec's
+// half of the latent is picked after.
+struct WideTile {
+    uint32_t lat[16];
+    uint4 res;
+    float scale, lambda;
+    uint32_t flagw, gsw;
+};
+
+__device__ __forceinline__ void wide_load_tile(__amdgpu_buffer_rsrc_t rsrc, uint32_t n, uint32_t g,
+                                               WideTile& t) {
+    // Default cache policy: the two lane halves read parts of the same tile
+    // in separate instructions, and the second must find it in L2.
+    const uint32_t o = 128u * n;
 #pragma unroll
-    for (uint32_t k = 0; k < kWideRowsPerWave; ++k)
-        if (wv + 4u * k < rows) stage_f16_row(r.v0[k], r.v1[k], wv + 4u * k, q16, qexp);
+    for (int j = 0; j < 4; ++j) {
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o + 16u * j, 0, 0));
+        t.lat[4 * j] = v.x, t.lat[4 * j + 1] = v.y, t.lat[4 * j + 2] = v.z, t.lat[4 * j + 3] = v.w;
+    }
+    t.res = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o + 64u + 16u * g, 0, 0));
+    const uint2 m = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, o + 96u, 0, 0));
+    t.scale = __uint_as_float(m.x);
+    t.lambda = __uint_as_float(m.y);
+    t.flagw = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o + 116u, 0, 0);
+    t.gsw = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o + 120u + 4u * g, 0, 0);
+}
+
+// The lane's half of the latent: INT4 dwords 8 g .. 8 g + 7; TQ3 code
+// dwords 6 g .. 6 g + 5, then corr dwords 12 + 2 g, 13 + 2 g.
+template <int CLS>
+__device__ __forceinline__ void wide_pick_half(const uint32_t (&lat)[16], uint32_t g, uint32_t (&h)[8]) {
+    // a bit-select in asm: written as a select, the compiler indexes the
+    // latent array with g and moves it to scratch memory
+    const uint32_t gm = 0u - g;
 #pragma unroll
-    for (uint32_t k = 0; k < kMfmaMaxGroup * 8 / 256; ++k) {
-        const uint32_t i = threadIdx.x + 256u * k;
-        if (i < group * 8u) {
-            // inline asm store, as in stage_f16_row: no wait for the tile DMA
-            asm volatile("ds_write_b32 %0, %1" ::"v"(lds_byte_addr(qsl + i)), "v"(r.sw[k]) : "memory");
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t a = CLS == kClsInt4 ? lat[j] : lat[j < 6 ? j : 6 + j];
+        const uint32_t b = CLS == kClsInt4 ? lat[8 + j] : lat[j < 6 ? 6 + j : 8 + j];
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(h[j]) : "v"(gm), "v"(b), "v"(a));
+    }
+}
+
+// f16 B operands of K-step ks for the lane's tile (see above).
+__device__ __forceinline__ v8h wide_b_int4(uint32_t x, uint32_t magic, v2h off, v2h g2) {
+    constexpr uint32_t M = 0x00F000F0u;  // nibbles k, k + 4 at bits 4..7 / 20..23
+    const uint32_t d[4] = {((x << 4) & M) | magic, (x & M) | magic, ((x >> 4) & M) | magic,
+                           ((x >> 8) & M) | magic};
+    uint32_t r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = __builtin_bit_cast(uint32_t, (as_v2h(d[k]) + off) * g2);
+    return __builtin_bit_cast(v8h, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// x: the window's 24 code bits (code of dim j at 3 j); cm: the window's
+// corr-LUT entry (corr bits placed under the codes, over the magic
+// exponents); off: minus (base + 7.5) per half (NOCORR: base + 7).
+__device__ __forceinline__ void wide_b_tq3(uint32_t x, uint4 cm, v2h off, v2h g2, v8h& bm, v8h& be) {
+    constexpr uint32_t M = 0x001C01C0u;  // code of dim k at bits 6..8, of dim k + 4 at 18..20
+    const uint32_t d[4] = {((x << 6) & M) | cm.x, ((x << 3) & M) | cm.y, (x & M) | cm.z,
+                           ((x >> 3) & M) | cm.w};
+    uint32_t m[4], e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const v2h lh = as_v2h(d[k]) + off;  // L / 2, exact
+        const v2h p = lh * g2;               // f16(L * gs)
+        m[k] = __builtin_bit_cast(uint32_t, p);
+        e[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(lh, g2, -p));  // exact
+    }
+    bm = __builtin_bit_cast(v8h, make_uint4(m[0], m[1], m[2], m[3]));
+    be = __builtin_bit_cast(v8h, make_uint4(e[0], e[1], e[2], e[3]));
+}
+
+// 24-bit code window of K-step ks from the lane's six code dwords.
+__device__ __forceinline__ uint32_t wide_code_window(const uint32_t* cd, int ks) {
+    const int b = 24 * ks, j = b >> 5, sh = b & 31;
+    return sh == 0 ? cd[j] : sh <= 8 ? cd[j] >> sh : __builtin_amdgcn_alignbit(cd[j + 1], cd[j], sh);
+}
+
+// Where a block's scores go.
+struct WideOut {
+    float* out;     // the row's scores, [group][n_tok]
+    uint32_t n_tok, group;
+};
+
+// One codec-uniform INT4 or TQ3 block of 32 tiles against NQ = 32 NQB
+// queries.
+template <int CLS, uint32_t NQB>
+__device__ __forceinline__ void wide_score_block(const char* lds_img, const uint2* pm1_lut,
+                                                 const uint4* corr_lut, const WideTile& cur,
+                                                 const WideOut& o, uint32_t tile0, uint32_t n_valid) {
+    constexpr uint32_t NQ = 32u * NQB;
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 5, col = lane & 31u;
+    const uint4* H = reinterpret_cast<const uint4*>(lds_img);
+    const uint4* P = reinterpret_cast<const uint4*>(lds_img + wide_off_p(NQ));
+    const float* E = reinterpret_cast<const float*>(lds_img + wide_off_e(NQ));
+    uint32_t magic = CLS == kClsInt4 ? 0x54005400u : 0u;  // 64.0 in both halves
+    asm volatile("" : "+v"(magic));
+    const uint32_t flags = cur.flagw >> 16;
+    uint32_t h[8];
+    wide_pick_half<CLS>(cur.lat, g, h);
+    const bool nocorr = (flags & kFlagNoCorr) != 0;
+    if constexpr (CLS == kClsTQ3) {
+        if (nocorr) h[6] = h[7] = 0u;
+    }
+    auto b_of = [&](int ks, v8h& bm, v8h& be) {
+        // group of K-step ks: 4 g + ks / 2 (byte ks / 2 of gsw)
+        const _Float16 gv = (_Float16)(float)((cur.gsw >> (8 * (ks >> 1))) & 0xFFu);
+        if constexpr (CLS == kClsInt4) {
+            const v2h off = v2h{(_Float16)-72.0f, (_Float16)-72.0f};
+            bm = wide_b_int4(h[ks], magic, off, v2h{gv, gv});
+            be = bm;
+        } else {
+            const uint32_t cr = (h[6 + (ks >> 2)] >> (8 * (ks & 3))) & 0xFFu;
+            const uint4 cm = corr_lut[cr];
+            const v2h off = nocorr ? v2h{(_Float16)-39.0f, (_Float16)-519.0f}
+                                   : v2h{(_Float16)-39.5f, (_Float16)-519.5f};
+            const _Float16 g2v = gv + gv;
+            wide_b_tq3(wide_code_window(h, ks), cm, off, v2h{g2v, g2v}, bm, be);
+        }
+    };
+    auto a_of = [&](int ks, uint32_t qb, v8h& ah, v8h& al) {
+        const uint32_t ia = ((uint32_t)ks * 2u * 2u + g) * NQ + 32u * qb + col;
+        ah = __builtin_bit_cast(v8h, H[ia]);
+        al = __builtin_bit_cast(v8h, H[ia + 2u * NQ]);
+    };
+    // The A operands of step ks + 1 are read from LDS during step ks; B
+    // needs no copy ahead (the MFMAs of step ks run while the decode of
+    // step ks + 1 issues). The scheduling barrier at the end of each step
+    // keeps the compiler from hoisting later steps' LDS reads (and their
+    // registers) above it.
+    v16f acc[NQB];
+#pragma unroll
+    for (uint32_t qb = 0; qb < NQB; ++qb) acc[qb] = v16f{};
+    v8h ah[NQB], al[NQB];
+#pragma unroll
+    for (uint32_t qb = 0; qb < NQB; ++qb) a_of(0, qb, ah[qb], al[qb]);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        v8h bm, be, ah_n[NQB], al_n[NQB];
+        b_of(ks, bm, be);
+        if (ks < 7) {
+#pragma unroll
+            for (uint32_t qb = 0; qb < NQB; ++qb) a_of(ks + 1, qb, ah_n[qb], al_n[qb]);
+        }
+#pragma unroll
+        for (uint32_t qb = 0; qb < NQB; ++qb) {
+            acc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[qb], bm, acc[qb], 0, 0, 0);
+            acc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[qb], bm, acc[qb], 0, 0, 0);
+            if constexpr (CLS == kClsTQ3)
+                acc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[qb], be, acc[qb], 0, 0, 0);
+        }
+        if (ks < 7) {
+#pragma unroll
+            for (uint32_t qb = 0; qb < NQB; ++qb) ah[qb] = ah_n[qb], al[qb] = al_n[qb];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Residual term and epilogue, one query block at a time (one block's
+    // i8 accumulators live at once): 16 sign bits per K-chunk kc, bits
+    // 16 kc .. of the lane's 128, expanded to +-1 bytes one chunk ahead.
+    const uint32_t rw[4] = {cur.res.x, cur.res.y, cur.res.z, cur.res.w};
+    auto bt_of = [&](int kc) {
+        const uint32_t w = rw[kc >> 1] >> (16 * (kc & 1));
+        const uint2 lo = pm1_lut[w & 0xFFu], hi = pm1_lut[(w >> 8) & 0xFFu];
+        return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+    };
+    const float lvl = CLS == kClsInt4 ? 1.0f : 0.25f;
+    const float s = cur.scale * (1.0f / 255.0f) * lvl;
+    const float lam = (flags & kFlagWarm) ? 0.0f : cur.lambda;
+    const uint32_t t = tile0 + col;
+#pragma unroll
+    for (uint32_t qb = 0; qb < NQB; ++qb) {
+        auto aq_of = [&](int kc) {
+            return __builtin_bit_cast(v4i, P[((uint32_t)kc * 2u + g) * NQ + 32u * qb + col]);
+        };
+        v16i dot = v16i{};
+        v4i bt = bt_of(0), aq = aq_of(0);
+#pragma unroll
+        for (int kc = 0; kc < 8; ++kc) {
+            v4i bt_n = bt, aq_n = aq;
+            if (kc < 7) bt_n = bt_of(kc + 1), aq_n = aq_of(kc + 1);
+            dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bt, dot, 0, 0, 0);
+            bt = bt_n, aq = aq_n;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float sc[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 qe = *reinterpret_cast<const float4*>(E + 32u * qb + 8u * j + 4u * g);
+            const float q4[4] = {qe.x, qe.y, qe.z, qe.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sc[4 * j + r] = fmaf(lam, (float)dot[4 * j + r], acc[qb][4 * j + r] * (s * q4[r]));
+        }
+        // Accumulator i is query row 32 qb + 4 g + 8 (i / 4) + i % 4. The
+        // stores go through a buffer over the block's rows that exist
+        // (n_tok < 2^25 keeps every offset below 2^32): with all 32 rows,
+        // the row offset rides in the SGPR operand; otherwise in the VGPR
+        // operand, where the range check drops rows at or past `group`.
+        const uint32_t rows = o.group - 32u * qb < 32u ? o.group - 32u * qb : 32u;
+        const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+            o.out + (size_t)32u * qb * o.n_tok, 0, __builtin_amdgcn_readfirstlane(rows * o.n_tok * 4u),
+            0x00020000);
+        const uint32_t voff = (4u * g * o.n_tok + t) * 4u;
+        if (col < n_valid) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t di = (8u * (i >> 2) + (i & 3)) * o.n_tok * 4u;
+                if (rows == 32u)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc[i]), ors, voff,
+                                                          __builtin_amdgcn_readfirstlane(di), kCachePolicyNT);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc[i]), ors, voff + di, 0,
+                                                          kCachePolicyNT);
+            }
         }
     }
 }
 
-// Dynamic LDS of score_rows_wide_kernel: f16 hi/lo queries, their 2^e
-// factors and the queries' sign words (no f32 copy).
-__host__ __device__ constexpr size_t wide_staging_bytes(uint32_t group) {
-    return (size_t)staging_rows(group) * (kQStrideH * 2u + 4u) + (size_t)group * 32u;
-}
-// The staging as an image in global memory, rounded up to whole 1 KiB DMA
-// blocks (one wave-wide 16-B-per-lane load each).
-__host__ __device__ constexpr size_t wide_image_bytes(uint32_t group) {
-    return (wide_staging_bytes(group) + 1023u) & ~(size_t)1023u;
-}
+// Scoring of tile rows for 16 < group <= kMfmaMaxGroup. Workgroups of 8
+// waves stay resident and loop over the row's 512-tile chunks (chunk
+// blockIdx.x + k gridDim.x); wave w takes the chunk's 32-tile blocks 2w and
+// 2w + 1. The workgroup builds the row's query image in LDS once
+// (wide_stage_lds). A codec-uniform INT4 or TQ3 block runs
+// wide_score_block, any other block the per-lane path (lanes 0..31, one
+// tile each).
+constexpr uint32_t kWideChunk = 512;
+constexpr uint32_t kWideMaxTok = 1u << 25;  // longer rows take score_rows_kernel
 
-// One workgroup per row: the row's wide staging (f16 hi/lo queries, 2^e
-// factors, sign words), built in LDS exactly as score_rows_wide_kernel reads
-// it and copied out as an image that the scoring workgroups load with DMA.
-__global__ __launch_bounds__(256) void stage_wide_image_kernel(const float* __restrict__ qc,
-                                                               const uint32_t* __restrict__ qs,
-                                                               uint32_t group,
-                                                               uint4* __restrict__ img) {
-    extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_image_bytes(group)
-    const uint32_t row = blockIdx.x;
-    const size_t qrow0 = (size_t)row * group;
-    const uint32_t rows_alloc = staging_rows(group);
-    uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
-    float* qexp = reinterpret_cast<float*>(q16 + rows_alloc * kQStrideH);
-    uint32_t* qsl = reinterpret_cast<uint32_t*>(qexp + rows_alloc);
-    const uint32_t n16 = (uint32_t)(wide_image_bytes(group) / 16);
-    uint4* l4 = reinterpret_cast<uint4*>(qlds);
-    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) l4[i] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    WideQueryRegs qr;
-    wide_stage_issue(qc, qs, qrow0, group, qr);
-    wide_stage_commit(qr, group, q16, qexp, qsl);
-    __syncthreads();
-    uint4* out = img + (size_t)row * n16;
-    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) out[i] = l4[i];
-}
-
-// Scoring of tile rows for 16 < group <= kMfmaMaxGroup: the coalesced tile
-// fetch of score_rows_fast_kernel; INT4 and TQ3 waves run score_wave_wide,
-// waves of other codecs the per-lane path.
-__global__ __launch_bounds__(256) void score_rows_wide_kernel(
+template <uint32_t NQB>
+__global__ __launch_bounds__(512, 4) void score_rows_wide_kernel(
     const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
-    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores,
-    const uint4* __restrict__ img) {
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
     __shared__ float cb[16];
-    __shared__ uint4 tile_lds[4][512];
     __shared__ uint2 pm1_lut[256];
+    __shared__ uint4 corr_lut[256];
     extern __shared__ __attribute__((aligned(16))) float qlds[];  // wide_image_bytes(group)
     const uint32_t row = blockIdx.y;
     const size_t qrow0 = (size_t)row * group;
-    const uint32_t rows_alloc = staging_rows(group);
-    uint16_t* q16 = reinterpret_cast<uint16_t*>(qlds);
-    float* qexp = reinterpret_cast<float*>(q16 + rows_alloc * kQStrideH);
-    uint32_t* qsl = reinterpret_cast<uint32_t*>(qexp + rows_alloc);
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 5, col = lane & 31u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
-    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
-    // The row's staging image (stage_wide_image_kernel) goes into LDS by
-    // DMA, 1 KiB per wave instruction, ahead of the tile DMA; each wave then
-    // waits for its image loads alone (the 8 tile loads stay in flight)
-    // before the barrier that publishes the image to the other waves.
-    {
-        const uint32_t nblk_img = (uint32_t)(wide_image_bytes(group) / 1024);
-        const uint32_t lane = threadIdx.x & 63u;
-        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint4*>(img + (size_t)row * nblk_img * 64), 0,
-            __builtin_amdgcn_readfirstlane(nblk_img * 1024u), 0x00020000);
-        for (uint32_t b = wave; b < nblk_img; b += 4u)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(qlds) + 1024u * b),
-                16, lane * 16u, b * 1024u, 0, 0);
-    }
-    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+    const uint32_t n_chunks = (n_tok + kWideChunk - 1) / kWideChunk;
+    wide_stage_lds<NQB>(qc, qs, qrow0, group, reinterpret_cast<char*>(qlds));
+    // Block i of this wave: chunk blockIdx.x + (i / 2) gridDim.x, tiles
+    // 64 wave + 32 (i % 2) of it. Tiles at or past n_valid read as zero.
+    const uint4* row_tiles = tiles + (size_t)row * n_tok * 8;
+    auto block_tile0 = [&](uint32_t i) {
+        return (blockIdx.x + (i >> 1) * gridDim.x) * kWideChunk + 64u * wave + 32u * (i & 1u);
+    };
+    auto block_rsrc = [&](uint32_t tile0) {
+        const uint32_t nv = tile0 < n_tok ? n_tok - tile0 : 0u;
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint4*>(row_tiles + (size_t)tile0 * 8), 0,
+            __builtin_amdgcn_readfirstlane((nv < 32u ? nv : 32u) * 128u), 0x00020000);
+    };
+    auto block_exists = [&](uint32_t i) {
+        return blockIdx.x + (i >> 1) * gridDim.x < n_chunks && block_tile0(i) < n_tok;
+    };
     stage_codebook(cb);
-    pm1_lut[threadIdx.x] = pm1_bytes(threadIdx.x);
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    if (threadIdx.x < 256u) {
+        const uint32_t b = threadIdx.x;
+        pm1_lut[b] = pm1_bytes(b);
+        uint32_t e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            e[k] = (((b >> k) & 1u) << 5) | (((b >> (k + 4)) & 1u) << 17) | 0x60005000u;
+        corr_lut[b] = make_uint4(e[0], e[1], e[2], e[3]);
+    }
     __syncthreads();
-    uint32_t w[32];
-    fetch_tiles_readback(tile_lds[wave], w);
-    const uint32_t t = wave0 + (threadIdx.x & 63u);
-    const bool valid = t < n_tok;
-    float* out = scores + qrow0 * n_tok;
-    const int cls = valid ? codec_class(w[29] >> 16) : -1;
-    const int c0 = __builtin_amdgcn_readfirstlane(cls);
-    const bool uniform = c0 >= 0 && __all(cls == c0 || cls < 0);
-    if (uniform && c0 == kClsInt4) {
-        score_wave_wide<kClsInt4>(tile_lds[wave], group, q16, qexp, qsl, pm1_lut, out, n_tok, wave0);
-        return;
+    const char* lds_img = reinterpret_cast<const char*>(qlds);
+    const WideOut o{scores + qrow0 * n_tok, n_tok, group};
+    // No block is loaded ahead: the 16 resident waves of a CU cover each
+    // other's load latency, and a tile held across the loop would cost the
+    // registers that keep 4 waves per SIMD.
+    for (uint32_t i = 0; block_exists(i); ++i) {
+        const uint32_t tile0 = block_tile0(i);
+        const uint32_t n_valid = n_tok - tile0;  // > 0
+        const __amdgpu_buffer_rsrc_t rs = block_rsrc(tile0);
+        WideTile cur;
+        wide_load_tile(rs, col, g, cur);
+        const int cls = codec_class(cur.flagw >> 16);
+        const int c0 = __builtin_amdgcn_readfirstlane(cls);  // lane 0's tile is valid
+        const bool uniform = __all(cls == c0 || col >= n_valid);
+        if (uniform && c0 == kClsInt4) {
+            wide_score_block<kClsInt4, NQB>(lds_img, pm1_lut, corr_lut, cur, o, tile0, n_valid);
+        } else if (uniform && c0 == kClsTQ3) {
+            wide_score_block<kClsTQ3, NQB>(lds_img, pm1_lut, corr_lut, cur, o, tile0, n_valid);
+        } else if (lane < 32u && col < n_valid) {
+            // per-lane path: lane L < 32 scores tile tile0 + L
+            uint32_t w[32];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint4 v = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, 128u * col + 16u * j, 0, 0));
+                w[4 * j] = v.x, w[4 * j + 1] = v.y, w[4 * j + 2] = v.z, w[4 * j + 3] = v.w;
+            }
+            score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, o.out, nullptr, n_tok, tile0 + col);
+        }
     }
-    if (uniform && c0 == kClsTQ3) {
-        score_wave_wide<kClsTQ3>(tile_lds[wave], group, q16, qexp, qsl, pm1_lut, out, n_tok, wave0);
-        return;
-    }
-    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
 // CCOS paged scoring on the fast path (pages of at least 64 tiles, group <=
@@ -3723,10 +3769,7 @@ __global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restr
 // ---------------------------------------------------------------------------
 // Launchers
 
-size_t score_rows_workspace_bytes(uint32_t n_rows, uint32_t group, bool exact, bool ham) {
-    const bool wide = !exact && !ham && group > kRegStageMaxGroup && group <= kMfmaMaxGroup;
-    return wide ? (size_t)n_rows * wide_image_bytes(group) : 0;
-}
+size_t score_rows_workspace_bytes(uint32_t, uint32_t, bool, bool) { return 0; }
 
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
@@ -3744,14 +3787,20 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
             score_rows_fast_kernel<4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= kRegStageMaxGroup)
             score_rows_fast_kernel<16><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
+        else if (n_tok >= kWideMaxTok)
+            score_rows_kernel<false, false><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
         else {
-            if (!workspace) return hipErrorInvalidValue;  // score_rows_workspace_bytes
-            uint4* img = static_cast<uint4*>(workspace);
-            stage_wide_image_kernel<<<n_rows, 256, wide_image_bytes(group), s>>>(qc, qsw, group, img);
-            const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            score_rows_wide_kernel<<<grid, 256, wide_image_bytes(group), s>>>(tp, n_tok, group, qc,
-                                                                            qsw, scores, img);
+            // resident workgroups: about two per CU over all rows, each
+            // looping over its row's 512-tile chunks
+            const uint32_t n_chunks = (n_tok + kWideChunk - 1) / kWideChunk;
+            const uint32_t per_row = std::max(1u, std::min(n_chunks, (512u + n_rows - 1) / n_rows));
+            const dim3 wgrid(per_row, n_rows);
+            if (group <= 32)
+                score_rows_wide_kernel<1><<<wgrid, 512, wide_image_bytes(group), s>>>(tp, n_tok, group, qc,
+                                                                                   qsw, scores);
+            else
+                score_rows_wide_kernel<2><<<wgrid, 512, wide_image_bytes(group), s>>>(tp, n_tok, group, qc,
+                                                                                   qsw, scores);
         }
         return hipGetLastError();
     }

@@ -21,8 +21,8 @@ constexpr uint32_t kMaxTopK = 256;
 constexpr uint32_t kTopkSeg = 16384;
 constexpr uint32_t kTopkMaxCandidates = 8192;
 
-// `workspace`: device memory of score_rows_workspace_bytes() (a staging image
-// per row for 16 < group <= 64 in fast mode; otherwise unused, may be null).
+// `workspace`: device memory of score_rows_workspace_bytes(), which no
+// scoring path needs at present (0 bytes; may be null).
 // `codec_hint`: the codec id the tiles were encoded with, or -1 if unknown;
 // it selects kernels only (kCodecInt4Single: the integer INT4 path for
 // group <= 4) and never changes a result.

@@ -253,13 +253,16 @@ def test_score_exact_bit_identical_and_hamming(s, torch, group):
 
 
 @pytest.mark.parametrize("group,codec", [(4, 0), (8, 2), (20, 4), (5, None), (24, 0), (64, 1),
-                                         (33, None), (40, "tq3_nocorr"), (17, 2)])
+                                         (33, None), (40, "tq3_nocorr"), (17, 2), (32, 0),
+                                         (64, "tq3_mix"), (48, "tq3_mix"), (64, 4)])
 def test_score_fast_streaming_ragged(s, torch, group, codec):
     # Many workgroups per row, a ragged last wave per row (n_tok not a
     # multiple of 64) and waves entirely past the end of the row. Groups
     # past 16 take the wide kernel (INT4 and TQ3 with and without the
-    # correction plane on 16x16x32 MFMA). codec None: random mixed-codec
-    # tiles, so waves fall back to the per-lane path.
+    # correction plane on 32x32 MFMA; 32 and 64 queries fill whole query
+    # blocks, 17..31, 33..63 leave rows of the last block unstored). codec
+    # None: random mixed-codec tiles, so waves fall back to the per-lane
+    # path. tq3_mix: TQ3 waves whose tiles mix corrected, NOCORR and WARM.
     n_rows, n_tok = 8, 50_001
     r = np.random.default_rng(1000 + group)
     if codec is None:
@@ -268,11 +271,16 @@ def test_score_fast_streaming_ragged(s, torch, group, codec):
         g = torch.Generator(device="cuda").manual_seed(group)
         keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
         with s.Model(seed=group) as m:
-            td = s.gpu_encode(m, keys, s.CODEC_TQ3 if codec == "tq3_nocorr" else codec,
+            td = s.gpu_encode(m, keys, s.CODEC_TQ3 if codec in ("tq3_nocorr", "tq3_mix") else codec,
                               n_kv_heads=n_rows)
         if codec == "tq3_nocorr":
             slots = torch.arange(n_rows * n_tok, dtype=torch.int32, device="cuda")
             s.gpu_ccos_apply(td, slots, 1)
+        if codec == "tq3_mix":
+            pick = np.random.default_rng(7).random(n_rows * n_tok)
+            for op, sel in ((1, pick < 0.5), (0, (pick > 0.4) & (pick < 0.7))):
+                slots = dev(torch, np.nonzero(sel)[0].astype(np.int32))
+                s.gpu_ccos_apply(td, slots, op)
     q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
     qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
     qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
