@@ -1254,34 +1254,35 @@ __device__ __forceinline__ void wide_score_block(const char* lds_img, const uint
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Residual term and epilogue, one query block at a time (one block's
-    // i8 accumulators live at once): 16 sign bits per K-chunk kc, bits
-    // 16 kc .. of the lane's 128, expanded to +-1 bytes one chunk ahead.
+    // Residual term: 16 sign bits per K-chunk kc, bits 16 kc .. of the
+    // lane's 128, expanded to +-1 bytes once for both query blocks.
     const uint32_t rw[4] = {cur.res.x, cur.res.y, cur.res.z, cur.res.w};
     auto bt_of = [&](int kc) {
         const uint32_t w = rw[kc >> 1] >> (16 * (kc & 1));
         const uint2 lo = pm1_lut[w & 0xFFu], hi = pm1_lut[(w >> 8) & 0xFFu];
         return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
     };
+    auto aq_of = [&](int kc, uint32_t qb) {
+        return __builtin_bit_cast(v4i, P[((uint32_t)kc * 2u + g) * NQ + 32u * qb + col]);
+    };
+    v16i dots[NQB];
+#pragma unroll
+    for (uint32_t qb = 0; qb < NQB; ++qb) dots[qb] = v16i{};
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc) {
+        const v4i bt = bt_of(kc);
+#pragma unroll
+        for (uint32_t qb = 0; qb < NQB; ++qb)
+            dots[qb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq_of(kc, qb), bt, dots[qb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     const float lvl = CLS == kClsInt4 ? 1.0f : 0.25f;
     const float s = cur.scale * (1.0f / 255.0f) * lvl;
     const float lam = (flags & kFlagWarm) ? 0.0f : cur.lambda;
     const uint32_t t = tile0 + col;
 #pragma unroll
     for (uint32_t qb = 0; qb < NQB; ++qb) {
-        auto aq_of = [&](int kc) {
-            return __builtin_bit_cast(v4i, P[((uint32_t)kc * 2u + g) * NQ + 32u * qb + col]);
-        };
-        v16i dot = v16i{};
-        v4i bt = bt_of(0), aq = aq_of(0);
-#pragma unroll
-        for (int kc = 0; kc < 8; ++kc) {
-            v4i bt_n = bt, aq_n = aq;
-            if (kc < 7) bt_n = bt_of(kc + 1), aq_n = aq_of(kc + 1);
-            dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bt, dot, 0, 0, 0);
-            bt = bt_n, aq = aq_n;
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        const v16i dot = dots[qb];
         float sc[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
