@@ -99,10 +99,12 @@ int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n
 /*
  * slha_gpu_score with the codec the caller encoded the tiles with
  * (SLHA_CODEC_*, or -1 if unknown; slha_gpu_score passes -1). The hint picks
- * kernels and never changes a result: tiles of another codec are still
- * scored by their own codec, only more slowly. With SLHA_CODEC_INT4 and
- * group <= 4 in SLHA_SCORE_FAST mode the scores come from the integer matrix
- * cores (queries carried to ~2^-23 relative, within the fast-mode tolerance).
+ * kernels only: tiles of another codec are still scored by their own codec,
+ * only more slowly, and every kernel meets the fast-mode tolerance (results
+ * may differ between kernels in the last bits). In SLHA_SCORE_FAST mode
+ * with group <= 4: SLHA_CODEC_INT4 scores on the integer matrix cores
+ * (queries carried to ~2^-23 relative); SLHA_CODEC_NF4 on f16 matrix cores
+ * with each NF4 level carried as an f16 hi + lo pair (~2^-22).
  * No counterpart in the reference, which dispatches per tile on its flags
  * (simd.rs:23-84); an unknown hint is SLHA_ERR_CODEC.
  */

@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <utility>
 
 namespace slha {
 
@@ -508,7 +509,9 @@ struct QueryRegs {
     float2 b[ROWS / 4];  // f16 copy: row wave + 4 k, dims (d, d + 4), d = f16_stage_dim(lane)
 };
 
-template <uint32_t ROWS>
+// NATURAL: the f16 copy holds dims (d, d + 1), d = 8 (lane / 4) + 2 (lane % 4),
+// i.e. K order (d0, d1, d2, d3 | d4, d5, d6, d7) per latent dword.
+template <uint32_t ROWS, bool NATURAL = false>
 __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t qrow0,
                                             uint32_t group, QueryRegs<ROWS>& r) {
     // Buffer loads over exactly the row's `group` queries: rows past `group`
@@ -527,13 +530,14 @@ __device__ __forceinline__ void stage_issue(const float* __restrict__ qc, size_t
         const uint32_t i = (threadIdx.x + 256u * k) & (ROWS * 32u - 1u);  // float4 index
         r.a[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16u * i, 0, 0));
     }
-    const uint32_t voff = 4u * f16_stage_dim(lane);
+    const uint32_t voff = 4u * (NATURAL ? 8u * (lane >> 2) + 2u * (lane & 3u) : f16_stage_dim(lane));
+    constexpr uint32_t second = NATURAL ? 4u : 16u;  // byte offset of the pair's second dim
 #pragma unroll
     for (uint32_t k = 0; k < ROWS / 4; ++k) {
         const uint32_t soff = (wv + 4u * k) * kDC * 4u;
         r.b[k] = make_float2(
             __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, soff + voff, 0, 0)),
-            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, soff + voff + 16u, 0, 0)));
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, soff + voff + second, 0, 0)));
     }
 }
 
@@ -892,6 +896,156 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
     float* out = scores + qrow0 * n_tok;
     if (score_wave_try_mfma(w, valid, group, qrow0, sq.q32, cb, sq.q16, sq.qexp, qs, out, n_tok, t))
         return;
+    if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
+}
+
+// NF4 fast path for group <= 4 (the launch takes it when the caller's
+// codec hint is NF4) on v_mfma_f32_4x4x4_16b_f16: lane = tile, 4 queries,
+// each 16-dim group accumulated on its own and added in with its scale gs.
+// One MFMA K-step covers the two dims (d0, d1) of a latent byte in four
+// slots (d0, d1, d0, d1):
+//  * B is a 256-entry LDS table indexed by the byte: the f16 hi halves of the
+//    two nibbles' NF4 levels (constants.rs:138-141), then their lo halves
+//    (hi + lo = level to ~2^-22). One 8-byte read is one B operand.
+//  * A is (q_hi[d0], q_hi[d1], q_hi[d0], q_hi[d1]) and, in a second MFMA,
+//    the same of q_lo: together (q_hi + q_lo)(L_hi + L_lo) over the pair.
+// All 16 blocks multiply the same 4 queries, so every MFMA broadcasts one
+// block's A operand to all (CBSZ 4): the tile's 128 A operands (64 bytes x
+// hi/lo), o = 2 (byte index) + half, live as 8 register pairs spread over
+// the lane blocks, operand o in pair o / 16 of block o % 16 (ABID), read
+// once per wave. A table entry is used as it is read: no VALU builds an
+// operand.
+constexpr uint32_t kNF4QStride = 128u * 8u + 16u;  // bytes per staged query
+
+template <int O>
+__device__ __forceinline__ v4f nf4_mfma(const uint2 (&a)[8], v4h b, v4f acc) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(v4h, a[O >> 4]), b, acc, 4, O & 15, 0);
+}
+
+// Group G (latent bytes 8G .. 8G + 7, dims 16G .. 16G + 15) accumulated on
+// its own, added in with gs.
+template <int G>
+__device__ __forceinline__ void nf4_group(const uint32_t* w, const uint2* lut, const uint2 (&a)[8],
+                                          v4f& dot) {
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    uint2 e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = lut[(w[2 * G + (j >> 2)] >> (8 * (j & 3))) & 0xFFu];
+    // byte 8G + j: A operands 2 (8G + j) (hi) and 2 (8G + j) + 1 (lo)
+#define SLHA_NF4_BYTE(J)                                                   \
+    acc = nf4_mfma<16 * G + 2 * (J)>(a, __builtin_bit_cast(v4h, e[J]), acc); \
+    acc = nf4_mfma<16 * G + 2 * (J) + 1>(a, __builtin_bit_cast(v4h, e[J]), acc);
+    SLHA_NF4_BYTE(0) SLHA_NF4_BYTE(1) SLHA_NF4_BYTE(2) SLHA_NF4_BYTE(3)
+    SLHA_NF4_BYTE(4) SLHA_NF4_BYTE(5) SLHA_NF4_BYTE(6) SLHA_NF4_BYTE(7)
+#undef SLHA_NF4_BYTE
+    const float gsf = gs_at(w + 30, G);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) dot[rr] = fmaf(acc[rr], gsf, dot[rr]);
+}
+
+template <int... G>
+__device__ __forceinline__ void nf4_groups(const uint32_t* w, const uint2* lut, const uint2 (&a)[8],
+                                           v4f& dot, std::integer_sequence<int, G...>) {
+    (nf4_group<G>(w, lut, a, dot), ...);
+}
+
+// qdup: per query kNF4QStride bytes, A operand o at byte 8 o.
+__device__ __forceinline__ void score_wave_nf4_f16(const uint32_t* w, bool valid, uint32_t group,
+                                                   size_t qrow0, const char* qdup,
+                                                   const float* qexp, const uint2* lut,
+                                                   const uint32_t* __restrict__ qs,
+                                                   float* __restrict__ out, size_t stride,
+                                                   uint32_t t) {
+    const uint32_t lane = threadIdx.x & 63u;
+    // lane 4b + r: operands 16k + b of query r, k = 0..7
+    const uint2* qa = reinterpret_cast<const uint2*>(qdup + (lane & 3u) * kNF4QStride) + (lane >> 2);
+    uint2 a[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = qa[16 * k];
+    v4f dot = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    nf4_groups(w, lut, a, dot, std::make_integer_sequence<int, 8>{});
+    const float s255 = __uint_as_float(w[24]) * (1.0f / 255.0f);
+    const float lambda = __uint_as_float(w[25]);
+    const bool warm = ((w[29] >> 16) & kFlagWarm) != 0;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        if ((uint32_t)rr < group) {
+            float sc = dot[rr] * (s255 * qexp[rr]);
+            const uint32_t h = hamming_words(w + 16, qs + (qrow0 + rr) * 8);
+            if (!warm) sc = fmaf(lambda, 256.0f - 2.0f * (float)h, sc);
+            if (valid) store_out(out + (size_t)rr * stride + t, sc);
+        }
+    }
+}
+
+// f16 hi/lo bits of an NF4 level: hi | lo << 16.
+__device__ __forceinline__ uint32_t nf4_level_pair(uint32_t n) {
+    const float l = nf4_level(n);
+    const _Float16 hi = (_Float16)l;
+    const _Float16 lo = (_Float16)(l - (float)hi);
+    return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
+// Scoring of rows of NF4 tiles, group <= 4: the tile fetch of
+// score_rows_fast_kernel, the queries staged for score_wave_nf4_f16 (wave j
+// stages query j, lane l converts dims 2l, 2l + 1 into A operands 2l and
+// 2l + 1; rows past `group` are zero), and score_wave_nf4_f16 for NF4
+// waves. Other waves take the per-lane path.
+__global__ __launch_bounds__(256) void score_rows_nf4_kernel(
+    const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
+    const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
+    __shared__ float cb[16];
+    __shared__ uint2 lut[256];
+    __shared__ uint4 tile_lds[4][512];
+    __shared__ __attribute__((aligned(16))) char qdup[4 * kNF4QStride];
+    __shared__ float qexp[4];
+    const uint32_t row = blockIdx.y;
+    const size_t qrow0 = (size_t)row * group;
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // query `wave`, dims (2 lane, 2 lane + 1), read as zero past `group`
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(qc + qrow0 * kDC), 0, __builtin_amdgcn_readfirstlane(group * kDC * 4u),
+        0x00020000);
+    const uint2 qv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   rq, wave * kDC * 4u + 8u * lane, 0, 0));
+    const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
+    const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
+    fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
+    stage_codebook(cb);
+    {
+        // byte b = n0 | n1 << 4: (hi(n0), hi(n1), lo(n0), lo(n1))
+        const uint32_t p0 = nf4_level_pair(threadIdx.x & 15u), p1 = nf4_level_pair(threadIdx.x >> 4);
+        lut[threadIdx.x] = make_uint2((p0 & 0xFFFFu) | (p1 << 16), (p0 >> 16) | (p1 & 0xFFFF0000u));
+    }
+    {
+        const float v0 = __uint_as_float(qv.x), v1 = __uint_as_float(qv.y);
+        const int e = stage_exponent(v0, v1);
+        const float inv = ldexpf(1.0f, -e);
+        const float d0 = v0 * inv, d1 = v1 * inv;
+        // Truncating f16 split: x - hi is exact in f32 and lo keeps 11 more bits.
+        const auto hi = __builtin_amdgcn_cvt_pkrtz(d0, d1);
+        const auto lo = __builtin_amdgcn_cvt_pkrtz(d0 - (float)hi.x, d1 - (float)hi.y);
+        const uint32_t h2 = __builtin_bit_cast(uint32_t, hi), l2 = __builtin_bit_cast(uint32_t, lo);
+        // operands 2 lane (hi) and 2 lane + 1 (lo); stored from inline asm,
+        // as in stage_f16_row: no wait for the tile DMA
+        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+        asm volatile("ds_write_b128 %0, %1" ::"v"(lds_byte_addr(qdup + wave * kNF4QStride + 16u * lane)),
+                     "v"(v4u{h2, h2, l2, l2})
+                     : "memory");
+        if (lane == 0) qexp[wave] = ldexpf(1.0f, e);
+    }
+    lds_barrier();
+    uint32_t w[32];
+    fetch_tiles_readback(tile_lds[wave], w);
+    const bool valid = t < n_tok;
+    float* out = scores + qrow0 * n_tok;
+    const int cls = valid ? codec_class(w[29] >> 16) : -1;
+    if (__all(cls == kClsNF4 || cls < 0) && __builtin_amdgcn_readfirstlane(cls) == kClsNF4) {
+        score_wave_nf4_f16(w, valid, group, qrow0, qdup, qexp, lut, qs, out, n_tok, t);
+        return;
+    }
     if (valid) score_dispatch<false, false>(w, group, qrow0, qc, qs, cb, out, nullptr, n_tok, t);
 }
 
@@ -3784,6 +3938,8 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
     if (!exact && !ham && group <= kMfmaMaxGroup) {
         if (group <= 4 && codec_hint == kCodecInt4Single)
             score_rows_int4_kernel<<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
+        else if (group <= 4 && codec_hint == kCodecNF4)
+            score_rows_nf4_kernel<<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= 4)
             score_rows_fast_kernel<4><<<grid, 256, 0, s>>>(tp, n_tok, group, qc, qsw, scores);
         else if (group <= kRegStageMaxGroup)

@@ -24,8 +24,9 @@ constexpr uint32_t kTopkMaxCandidates = 8192;
 // `workspace`: device memory of score_rows_workspace_bytes(), which no
 // scoring path needs at present (0 bytes; may be null).
 // `codec_hint`: the codec id the tiles were encoded with, or -1 if unknown;
-// it selects kernels only (kCodecInt4Single: the integer INT4 path for
-// group <= 4) and never changes a result.
+// it selects kernels only (for group <= 4: kCodecInt4Single the integer
+// INT4 path, kCodecNF4 the f16 NF4 path); every kernel meets the fast-mode
+// tolerance, and tiles of another codec are still scored by their codec.
 hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok, uint32_t group,
                              const float* qc, const uint64_t* qs, bool exact, float* scores,
                              uint32_t* ham, void* workspace, int codec_hint, hipStream_t s);

@@ -348,6 +348,72 @@ def test_score_int4_hint_integer_path(s, torch, group):
             assert_tol(hinted[qi, idx] / qscale[qi], ref / qscale[qi])
 
 
+@pytest.mark.parametrize("group", [1, 2, 3, 4])
+def test_score_nf4_hint_path(s, torch, group):
+    # slha_gpu_score_codec with the NF4 hint: the f16 NF4 path (group <= 4),
+    # levels as f16 hi + lo pairs. Keys with four x20 outlier channels (as
+    # C3's), ragged rows, ~30 % WARM tiles, tiny and huge queries compared
+    # at their own scale; against SCORE_EXACT on every pair and the oracle on
+    # sampled tokens of every row.
+    n_rows, n_tok = 3, 5_003
+    g = torch.Generator(device="cuda").manual_seed(91 + group)
+    keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
+    keys[..., [3, 17, 64, 100]] *= 20.0
+    keys = keys.to(torch.bfloat16)
+    r = np.random.default_rng(10 + group)
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    qscale = np.ones(n_rows * group)
+    qscale[0], qscale[-1] = 1e-30, 1e30
+    q = (q * qscale[:, None]).astype(np.float32)
+    with s.Model(seed=15 + group) as m:
+        td = s.gpu_encode(m, keys, s.CODEC_NF4, n_kv_heads=n_rows)
+        warm = np.flatnonzero(r.random(n_rows * n_tok) < 0.3).astype(np.int32)
+        s.gpu_ccos_apply(td, dev(torch, warm), 0)
+        qc, qs = s.gpu_prepare_queries(m, dev(torch, q))
+    hinted = s.gpu_score(td, qc, qs, group=group, codec_hint=s.CODEC_NF4).cpu().numpy()
+    plain = s.gpu_score(td, qc, qs, group=group).cpu().numpy()
+    exact = s.gpu_score(td, qc, qs, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+    qsc = qscale[:, None]
+    assert_tol(hinted / qsc, exact / qsc)
+    assert_tol(plain / qsc, exact / qsc)
+    tn = tiles_np(td)
+    qn, qsn = qc.cpu().numpy(), qs.cpu().numpy().view(np.uint64)
+    idx = np.r_[0:80, 2_000:2_064, n_tok - 80:n_tok]
+    for row in range(n_rows):
+        for j in range(group):
+            qi = row * group + j
+            ref, _ = o.score(tn[row * n_tok + idx], qn[qi], qsn[qi])
+            assert np.array_equal(exact[qi, idx].view(np.uint32), ref.view(np.uint32))
+            assert_tol(hinted[qi, idx] / qscale[qi], ref / qscale[qi])
+
+
+@pytest.mark.parametrize("case", ["mixed_codecs", "int4_tiles", "one_int4_tile"])
+def test_score_nf4_hint_fallback(s, torch, case):
+    # The NF4 hint on tiles that are not all NF4: such waves score on the
+    # paths of the unhinted kernel; results match SCORE_EXACT either way.
+    n_rows, n_tok, group = 2, 4_100, 4
+    r = np.random.default_rng(hash(case) % 1000)
+    if case == "mixed_codecs":
+        td = dev(torch, random_tiles(n_rows * n_tok, 12).view(np.uint8).reshape(n_rows, n_tok, 128))
+    else:
+        g = torch.Generator(device="cuda").manual_seed(4)
+        keys = torch.randn((n_rows, n_tok, 128), device="cuda", generator=g)
+        codec = s.CODEC_INT4_GROUPED if case == "int4_tiles" else s.CODEC_NF4
+        with s.Model(seed=10) as m:
+            td = s.gpu_encode(m, keys, codec, n_kv_heads=n_rows)
+        if case == "one_int4_tile":  # tile 33 of wave 1 loses its NF4 flag
+            tn = td.cpu().numpy().reshape(-1, 128).copy()
+            tn[64 + 33, 118] &= 0xFD
+            td = dev(torch, tn.reshape(n_rows, n_tok, 128))
+    q = r.normal(size=(n_rows * group, 128)).astype(np.float32)
+    qs = r.integers(0, 2**63, (n_rows * group, 4), dtype=np.uint64)
+    qd, qsd = dev(torch, q), dev(torch, qs.view(np.int64))
+    hinted = s.gpu_score(td, qd, qsd, group=group, codec_hint=s.CODEC_NF4).cpu().numpy()
+    exact = s.gpu_score(td, qd, qsd, group=group, mode=s.SCORE_EXACT).cpu().numpy()
+    assert np.isfinite(hinted).all()
+    assert_tol(hinted, exact)
+
+
 @pytest.mark.parametrize("case", ["mx_int4", "mixed_codecs", "one_nf4_tile", "one_tile_gs", "nan_query"])
 def test_score_int4_hint_fallback(s, torch, case):
     # The INT4 hint on tiles that do not all fit the integer path: a wave with
