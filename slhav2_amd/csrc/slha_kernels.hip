@@ -902,49 +902,54 @@ __global__ __launch_bounds__(256) void score_rows_fast_kernel(
 // NF4 fast path for group <= 4 (the launch takes it when the caller's
 // codec hint is NF4) on v_mfma_f32_4x4x4_16b_f16: lane = tile, 4 queries,
 // each 16-dim group accumulated on its own and added in with its scale gs.
-// One MFMA K-step covers the two dims (d0, d1) of a latent byte in four
-// slots (d0, d1, d0, d1):
+// Per latent byte (dims d0 = 2i, d1 = 2i + 1, nibbles n0, n1), one MFMA
+// K-step of four slots:
 //  * B is a 256-entry LDS table indexed by the byte: the f16 hi halves of the
 //    two nibbles' NF4 levels (constants.rs:138-141), then their lo halves
 //    (hi + lo = level to ~2^-22). One 8-byte read is one B operand.
-//  * A is (q_hi[d0], q_hi[d1], q_hi[d0], q_hi[d1]) and, in a second MFMA,
-//    the same of q_lo: together (q_hi + q_lo)(L_hi + L_lo) over the pair.
-// All 16 blocks multiply the same 4 queries, so every MFMA broadcasts one
-// block's A operand to all (CBSZ 4): the tile's 128 A operands (64 bytes x
-// hi/lo), o = 2 (byte index) + half, live as 8 register pairs spread over
-// the lane blocks, operand o in pair o / 16 of block o % 16 (ABID), read
-// once per wave. A table entry is used as it is read: no VALU builds an
-// operand.
-constexpr uint32_t kNF4QStride = 128u * 8u + 16u;  // bytes per staged query
+//  * A is (q_hi[d0], q_hi[d1], q_hi[d0], q_hi[d1]): q_hi (L_hi + L_lo) over
+//    the pair.
+// and per pair of bytes one more K-step for q_lo, the query's low f16 half:
+// A = q_lo of the four dims, B = the two entries' hi halves, so q_lo L_hi.
+// The q_lo L_lo term left out is below 2^-22 of each product. All 16 blocks
+// multiply the same 4 queries, so every MFMA broadcasts one block's A
+// operand to all (CBSZ 4): the 96 A operands (64 bytes' q_hi, then 32 byte
+// pairs' q_lo) live as 6 register pairs spread over the lane blocks,
+// operand o in pair o / 16 of block o % 16 (ABID), read once per wave.
+// Table entries are used as they are read: no VALU builds an operand.
+constexpr uint32_t kNF4QStride = 96u * 8u + 16u;  // bytes per staged query
+constexpr int kNF4LoOperand = 64;                 // first q_lo operand
 
 template <int O>
-__device__ __forceinline__ v4f nf4_mfma(const uint2 (&a)[8], v4h b, v4f acc) {
+__device__ __forceinline__ v4f nf4_mfma(const uint2 (&a)[6], v4h b, v4f acc) {
     return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(v4h, a[O >> 4]), b, acc, 4, O & 15, 0);
 }
 
 // Group G (latent bytes 8G .. 8G + 7, dims 16G .. 16G + 15) accumulated on
 // its own, added in with gs.
 template <int G>
-__device__ __forceinline__ void nf4_group(const uint32_t* w, const uint2* lut, const uint2 (&a)[8],
+__device__ __forceinline__ void nf4_group(const uint32_t* w, const uint2* lut, const uint2 (&a)[6],
                                           v4f& dot) {
     v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     uint2 e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) e[j] = lut[(w[2 * G + (j >> 2)] >> (8 * (j & 3))) & 0xFFu];
-    // byte 8G + j: A operands 2 (8G + j) (hi) and 2 (8G + j) + 1 (lo)
-#define SLHA_NF4_BYTE(J)                                                   \
-    acc = nf4_mfma<16 * G + 2 * (J)>(a, __builtin_bit_cast(v4h, e[J]), acc); \
-    acc = nf4_mfma<16 * G + 2 * (J) + 1>(a, __builtin_bit_cast(v4h, e[J]), acc);
-    SLHA_NF4_BYTE(0) SLHA_NF4_BYTE(1) SLHA_NF4_BYTE(2) SLHA_NF4_BYTE(3)
-    SLHA_NF4_BYTE(4) SLHA_NF4_BYTE(5) SLHA_NF4_BYTE(6) SLHA_NF4_BYTE(7)
-#undef SLHA_NF4_BYTE
+    // bytes 8G + 2P, 8G + 2P + 1: q_hi operands 8G + 2P, 8G + 2P + 1, then
+    // q_lo operand 64 + 4G + P
+#define SLHA_NF4_PAIR(P)                                                                   \
+    acc = nf4_mfma<8 * G + 2 * (P)>(a, __builtin_bit_cast(v4h, e[2 * (P)]), acc);          \
+    acc = nf4_mfma<8 * G + 2 * (P) + 1>(a, __builtin_bit_cast(v4h, e[2 * (P) + 1]), acc);  \
+    acc = nf4_mfma<kNF4LoOperand + 4 * G + (P)>(                                           \
+        a, __builtin_bit_cast(v4h, make_uint2(e[2 * (P)].x, e[2 * (P) + 1].x)), acc);
+    SLHA_NF4_PAIR(0) SLHA_NF4_PAIR(1) SLHA_NF4_PAIR(2) SLHA_NF4_PAIR(3)
+#undef SLHA_NF4_PAIR
     const float gsf = gs_at(w + 30, G);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) dot[rr] = fmaf(acc[rr], gsf, dot[rr]);
 }
 
 template <int... G>
-__device__ __forceinline__ void nf4_groups(const uint32_t* w, const uint2* lut, const uint2 (&a)[8],
+__device__ __forceinline__ void nf4_groups(const uint32_t* w, const uint2* lut, const uint2 (&a)[6],
                                            v4f& dot, std::integer_sequence<int, G...>) {
     (nf4_group<G>(w, lut, a, dot), ...);
 }
@@ -957,11 +962,11 @@ __device__ __forceinline__ void score_wave_nf4_f16(const uint32_t* w, bool valid
                                                    float* __restrict__ out, size_t stride,
                                                    uint32_t t) {
     const uint32_t lane = threadIdx.x & 63u;
-    // lane 4b + r: operands 16k + b of query r, k = 0..7
+    // lane 4b + r: operands 16k + b of query r, k = 0..5
     const uint2* qa = reinterpret_cast<const uint2*>(qdup + (lane & 3u) * kNF4QStride) + (lane >> 2);
-    uint2 a[8];
+    uint2 a[6];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) a[k] = qa[16 * k];
+    for (int k = 0; k < 6; ++k) a[k] = qa[16 * k];
     v4f dot = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     nf4_groups(w, lut, a, dot, std::make_integer_sequence<int, 8>{});
     const float s255 = __uint_as_float(w[24]) * (1.0f / 255.0f);
@@ -979,8 +984,7 @@ __device__ __forceinline__ void score_wave_nf4_f16(const uint32_t* w, bool valid
 }
 
 // f16 hi/lo bits of an NF4 level: hi | lo << 16.
-__device__ __forceinline__ uint32_t nf4_level_pair(uint32_t n) {
-    const float l = nf4_level(n);
+__device__ __forceinline__ uint32_t nf4_level_pair(float l) {
     const _Float16 hi = (_Float16)l;
     const _Float16 lo = (_Float16)(l - (float)hi);
     return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
@@ -988,9 +992,9 @@ __device__ __forceinline__ uint32_t nf4_level_pair(uint32_t n) {
 
 // Scoring of rows of NF4 tiles, group <= 4: the tile fetch of
 // score_rows_fast_kernel, the queries staged for score_wave_nf4_f16 (wave j
-// stages query j, lane l converts dims 2l, 2l + 1 into A operands 2l and
-// 2l + 1; rows past `group` are zero), and score_wave_nf4_f16 for NF4
-// waves. Other waves take the per-lane path.
+// stages query j, lane l converts dims 2l, 2l + 1 into q_hi operand l and
+// half of q_lo operand 64 + l / 2; rows past `group` are zero), and
+// score_wave_nf4_f16 for NF4 waves. Other waves take the per-lane path.
 __global__ __launch_bounds__(256) void score_rows_nf4_kernel(
     const uint4* __restrict__ tiles, uint32_t n_tok, uint32_t group,
     const float* __restrict__ qc, const uint32_t* __restrict__ qs, float* __restrict__ scores) {
@@ -1013,11 +1017,16 @@ __global__ __launch_bounds__(256) void score_rows_nf4_kernel(
     const uint32_t wave0 = blockIdx.x * blockDim.x + 64u * wave;
     const uint32_t n_valid = wave0 < n_tok ? n_tok - wave0 : 0u;
     fetch_tiles_lds(tiles + ((size_t)row * n_tok + wave0) * 8, n_valid, tile_lds[wave]);
-    stage_codebook(cb);
     {
-        // byte b = n0 | n1 << 4: (hi(n0), hi(n1), lo(n0), lo(n1))
-        const uint32_t p0 = nf4_level_pair(threadIdx.x & 15u), p1 = nf4_level_pair(threadIdx.x >> 4);
+        // byte b = n0 | n1 << 4: (hi(n0), hi(n1), lo(n0), lo(n1)). One level
+        // a lane (the select tree runs as branches under a divergent index):
+        // lane l holds level l & 15, and the level n1 = b >> 4 comes from
+        // lane n1 of the same wave.
+        const float lv = nf4_level(lane & 15u);
+        const uint32_t p0 = nf4_level_pair(lv);
+        const uint32_t p1 = (uint32_t)__shfl((int)p0, (int)(threadIdx.x >> 4));
         lut[threadIdx.x] = make_uint2((p0 & 0xFFFFu) | (p1 << 16), (p0 >> 16) | (p1 & 0xFFFF0000u));
+        if (threadIdx.x < 16) cb[threadIdx.x] = lv;
     }
     {
         const float v0 = __uint_as_float(qv.x), v1 = __uint_as_float(qv.y);
@@ -1028,11 +1037,13 @@ __global__ __launch_bounds__(256) void score_rows_nf4_kernel(
         const auto hi = __builtin_amdgcn_cvt_pkrtz(d0, d1);
         const auto lo = __builtin_amdgcn_cvt_pkrtz(d0 - (float)hi.x, d1 - (float)hi.y);
         const uint32_t h2 = __builtin_bit_cast(uint32_t, hi), l2 = __builtin_bit_cast(uint32_t, lo);
-        // operands 2 lane (hi) and 2 lane + 1 (lo); stored from inline asm,
-        // as in stage_f16_row: no wait for the tile DMA
-        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-        asm volatile("ds_write_b128 %0, %1" ::"v"(lds_byte_addr(qdup + wave * kNF4QStride + 16u * lane)),
-                     "v"(v4u{h2, h2, l2, l2})
+        // q_hi operand `lane` (byte 8 lane) and half of q_lo operand
+        // 64 + lane / 2 (byte 512 + 4 lane); stored from inline asm, as in
+        // stage_f16_row: no wait for the tile DMA
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        const uint32_t qa = lds_byte_addr(qdup + wave * kNF4QStride);
+        asm volatile("ds_write_b64 %0, %1\n\tds_write_b32 %2, %3" ::"v"(qa + 8u * lane), "v"(v2u{h2, h2}),
+                     "v"(qa + 8u * kNF4LoOperand + 4u * lane), "v"(l2)
                      : "memory");
         if (lane == 0) qexp[wave] = ldexpf(1.0f, e);
     }
