@@ -299,7 +299,8 @@ def run_c3(args) -> int:
     with s.Model(seed=0x5EED0004, rht=False, residual_mode=s.RESIDUAL_R) as m:
         qc, qs = s.gpu_prepare_queries(m, q)
         exact = torch.empty_like(scores)
-        for name, codec in (("nf4", s.CODEC_NF4), ("mx_int4", s.CODEC_INT4_GROUPED)):
+        for name, codec, kernel in (("nf4", s.CODEC_NF4, "slha::score_rows_nf4_kernel"),
+                                    ("mx_int4", s.CODEC_INT4_GROUPED, "slha::score_rows_fast_kernel<4u>")):
             enc_ms = timed_once(lambda: s.gpu_encode(m, keys, codec, n_kv_heads=n_kv, out=tiles,
                                                      stream=stream), stream)
             score = s.lib.slha_gpu_score_codec
@@ -313,7 +314,7 @@ def run_c3(args) -> int:
             if not err <= 1e-3:
                 raise RuntimeError(f"C3 {name}: fast scores differ from the exact path ({err})")
             results[name] = {"ms_per_step": ms, "tiles_per_s": n_q * n_tok / (ms * 1e-3),
-                             "roofline": hbm_roofline(nbytes, ms, "slha::score_rows_fast_kernel<4u>", f"c3_{name}"),
+                             "roofline": hbm_roofline(nbytes, ms, kernel, f"c3_{name}"),
                              "encode_keys_per_s": rows * n_tok / (enc_ms * 1e-3),
                              "encode_ms": enc_ms, "fast_vs_exact_max_rel_err_all_pairs": err}
             if not args.no_cpu_baseline:
