@@ -133,7 +133,19 @@ struct DeviceProjection {
     const void* zpack = nullptr;  // head_dim-128 models: kZPackBytes, MFMA operand pack of Z
     float cert_scale = 0.0f;      // build_projection_pack's scale
     const float* p = nullptr;     // learned models: [128][d]
+    const float* p4 = nullptr;    // learned models: P interleaved by 4 columns, [ceil(d/4)][128][4]
+    const float* z4 = nullptr;    // learned models: Z interleaved by 4 columns, [ceil(d_pad/4)][256][4]
 };
+
+// [R][n] row-major -> interleaved by 4 columns: element (r, i) at
+// ((i / 4) * R + r) * 4 + i % 4, zero past n (the layout of the learned
+// kernels' row dot products, one contiguous float4 per row and column group).
+static void interleave4(const float* m, size_t rows, size_t n, float* out) {
+    const size_t groups = (n + 3) / 4;
+    std::memset(out, 0, groups * rows * 4 * sizeof(float));
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t i = 0; i < n; ++i) out[((i / 4) * rows + r) * 4 + (i % 4)] = m[r * n + i];
+}
 
 // A head_dim-128 model (d = d_pad = 128, identity latent, Z [256][128]) or a
 // learned model loaded from a .slhw file (d > 128, P [128][d], Z [256][d_pad]).
@@ -168,17 +180,25 @@ struct Model {
         std::lock_guard<std::mutex> lock(mu);
         auto it = dev.find(device);
         if (it == dev.end()) {
-            // [Z][Z pack (head_dim-128 only)][diag][P (learned only)], 256-B aligned parts
+            // [Z][Z pack (head_dim-128 only)][diag][P, P4, Z4 (learned only)], 256-B
+            // aligned parts
             const size_t zb = align_up(z.size() * sizeof(float));
             const size_t pkb = learned ? 0 : kZPackBytes;
             const size_t db = align_up(d_pad * sizeof(float));
             const size_t pb = align_up(p.size() * sizeof(float));
-            std::vector<char> host(zb + pkb + db + pb, 0);
+            const size_t p4b = learned ? align_up((d + 3) / 4 * 128 * 4 * sizeof(float)) : 0;
+            const size_t z4b = learned ? align_up((d_pad + 3) / 4 * 256 * 4 * sizeof(float)) : 0;
+            std::vector<char> host(zb + pkb + db + pb + p4b + z4b, 0);
             std::memcpy(host.data(), z.data(), z.size() * sizeof(float));
             DeviceProjection dp;
             if (!learned) dp.cert_scale = build_projection_pack(z.data(), host.data() + zb);
             if (rht) std::memcpy(host.data() + zb + pkb, diag.data(), d_pad * sizeof(float));
-            if (learned) std::memcpy(host.data() + zb + pkb + db, p.data(), p.size() * sizeof(float));
+            if (learned) {
+                char* lp = host.data() + zb + pkb + db;
+                std::memcpy(lp, p.data(), p.size() * sizeof(float));
+                interleave4(p.data(), 128, d, reinterpret_cast<float*>(lp + pb));
+                interleave4(z.data(), 256, d_pad, reinterpret_cast<float*>(lp + pb + p4b));
+            }
             char* buf = nullptr;
             check_hip(hipMalloc(&buf, host.size()), "hipMalloc(projection)");
             check_hip(hipMemcpy(buf, host.data(), host.size(), hipMemcpyHostToDevice),
@@ -187,6 +207,8 @@ struct Model {
             dp.zpack = learned ? nullptr : buf + zb;
             dp.diag = rht ? reinterpret_cast<const float*>(buf + zb + pkb) : nullptr;
             dp.p = learned ? reinterpret_cast<const float*>(buf + zb + pkb + db) : nullptr;
+            dp.p4 = learned ? reinterpret_cast<const float*>(buf + zb + pkb + db + pb) : nullptr;
+            dp.z4 = learned ? reinterpret_cast<const float*>(buf + zb + pkb + db + pb + p4b) : nullptr;
             it = dev.emplace(device, std::make_pair(dp, static_cast<void*>(buf))).first;
         }
         return it->second.first;
@@ -198,6 +220,8 @@ struct Model {
         LearnedProjection lp;
         lp.p = dp.p;
         lp.z = dp.z;
+        lp.p4 = dp.p4;
+        lp.z4 = dp.z4;
         lp.diag = dp.diag;
         lp.d = (uint32_t)d;
         lp.d_pad = (uint32_t)d_pad;

@@ -2778,6 +2778,8 @@ struct LearnedArgs {
     const float* p;     // [128][d]
     const float* z;     // [256][d_pad]
     const float* diag;  // [d_pad] +-1, or null without RHT
+    const float4* p4;   // P interleaved by 4 columns: [ceil(d / 4)][128] float4
+    const float4* z4;   // Z interleaved by 4 columns: [ceil(d_pad / 4)][256] float4
     uint32_t d, d_pad;
     float rht_inv;      // 1 / sqrt(d_pad)
 };
@@ -2787,38 +2789,42 @@ __host__ __device__ constexpr size_t learned_lds_bytes(uint32_t d, uint32_t d_pa
     return ((size_t)d + d_pad + 128 + 32) * 4;
 }
 
-// Sequential f32 dot product sum_i row[i] * v[i], i = 0 .. n-1 (v in LDS).
-// The row (P or Z, read from L2) is loaded kDotBatch float4s at a time, all
-// issued before the batch's sequential adds, so one L2 latency is paid per
-// 64 terms instead of per 4; the sum order is unchanged.
+// Sequential f32 dot product sum_i M[r][i] * v[i], i = 0 .. n-1 (v in LDS),
+// of row r of an [R][n] matrix (P or Z, read from L2) stored interleaved by
+// 4 columns: element (r, i) at m4[(i / 4) R + r], component i % 4, zero past
+// n. Lanes holding consecutive rows read consecutive float4s, so each load
+// instruction of a wave reads 1 KiB contiguous (a row-major row per lane
+// touches 64 cache lines per load). The row is loaded kDotBatch float4s at a
+// time, all issued before the batch's sequential adds, so one L2 latency is
+// paid per 64 terms; the sum order is unchanged.
 constexpr uint32_t kDotBatch = 16;
 
-__device__ __forceinline__ float seq_dot(const float* __restrict__ row, const float* v, uint32_t n) {
+template <uint32_t R>
+__device__ __forceinline__ float seq_dot4(const float4* __restrict__ m4, uint32_t r, const float* v,
+                                          uint32_t n) {
+    const float4* col = m4 + r;
     float acc = 0.0f;
     uint32_t i = 0;
-    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
-        for (; i + 4 * kDotBatch <= n; i += 4 * kDotBatch) {
-            float4 r[kDotBatch];
+    for (; i + 4 * kDotBatch <= n; i += 4 * kDotBatch) {
+        float4 x[kDotBatch];
 #pragma unroll
-            for (uint32_t b = 0; b < kDotBatch; ++b) r[b] = *reinterpret_cast<const float4*>(row + i + 4 * b);
+        for (uint32_t b = 0; b < kDotBatch; ++b) x[b] = col[(size_t)(i / 4 + b) * R];
 #pragma unroll
-            for (uint32_t b = 0; b < kDotBatch; ++b) {
-                const uint32_t j = i + 4 * b;
-                acc += r[b].x * v[j];
-                acc += r[b].y * v[j + 1];
-                acc += r[b].z * v[j + 2];
-                acc += r[b].w * v[j + 3];
-            }
-        }
-        for (; i + 4 <= n; i += 4) {
-            const float4 r = *reinterpret_cast<const float4*>(row + i);
-            acc += r.x * v[i];
-            acc += r.y * v[i + 1];
-            acc += r.z * v[i + 2];
-            acc += r.w * v[i + 3];
+        for (uint32_t b = 0; b < kDotBatch; ++b) {
+            const uint32_t j = i + 4 * b;
+            acc += x[b].x * v[j];
+            acc += x[b].y * v[j + 1];
+            acc += x[b].z * v[j + 2];
+            acc += x[b].w * v[j + 3];
         }
     }
-    for (; i < n; ++i) acc += row[i] * v[i];
+    for (; i < n; i += 4) {
+        const float4 x = col[(size_t)(i / 4) * R];
+        acc += x.x * v[i];
+        if (i + 1 < n) acc += x.y * v[i + 1];
+        if (i + 2 < n) acc += x.z * v[i + 2];
+        if (i + 3 < n) acc += x.w * v[i + 3];
+    }
     return acc;
 }
 
@@ -2850,10 +2856,10 @@ __device__ __forceinline__ void block_rht(float* buf, const float* __restrict__ 
 
 // words[0..7] <- sign bits of Z . buf (bit s = 1 iff the sum is negative);
 // thread s computes row s, wave w's ballot is u64 word w. blockDim.x == 256.
-__device__ __forceinline__ void block_sign_bits(const float* buf, const float* __restrict__ z,
+__device__ __forceinline__ void block_sign_bits(const float* buf, const float4* __restrict__ z4,
                                                 uint32_t d_pad, uint32_t* words) {
     const uint32_t s = threadIdx.x;
-    const float acc = seq_dot(z + (size_t)s * d_pad, buf, d_pad);
+    const float acc = seq_dot4<kDS>(z4, s, buf, d_pad);
     const uint64_t m = __ballot(acc < 0.0f);
     if ((s & 63u) == 0) {
         words[2 * (s >> 6)] = (uint32_t)m;
@@ -2879,7 +2885,7 @@ __global__ __launch_bounds__(256) void learned_encode_kernel(const void* __restr
     for (uint64_t ki = blockIdx.x; ki < n_keys; ki += gridDim.x) {
         lds_load_vec(keys, dtype, ki, a.d, key);
         __syncthreads();
-        if (tid < 128) h[tid] = seq_dot(a.p + (size_t)tid * a.d, key, a.d);
+        if (tid < 128) h[tid] = seq_dot4<128>(a.p4, tid, key, a.d);
         __syncthreads();
         // Residual from the un-quantised latent.
         for (uint32_t i = tid; i < a.d; i += blockDim.x) {
@@ -2896,7 +2902,7 @@ __global__ __launch_bounds__(256) void learned_encode_kernel(const void* __restr
         }
         __syncthreads();  // sigma has read buf before the RHT rewrites it
         if (a.diag) block_rht(buf, a.diag, a.d_pad, a.rht_inv);
-        block_sign_bits(buf, a.z, a.d_pad, misc);
+        block_sign_bits(buf, a.z4, a.d_pad, misc);
         __syncthreads();
         if (tid == 0) {
             uint32_t lw[16], gsw[2];
@@ -2931,32 +2937,40 @@ __host__ __device__ constexpr size_t learned_lds_bytes2(uint32_t d, uint32_t d_p
 
 constexpr uint32_t kDot2Batch = 8;  // float4s per batch with two chains (register budget)
 
-__device__ __forceinline__ void seq_dot2(const float* __restrict__ row, const float* v0, const float* v1,
-                                         uint32_t n, float& a0, float& a1) {
+// seq_dot4 of one row against two vectors, one load of the row for both
+// chains (each chain in its own sequential order).
+template <uint32_t R>
+__device__ __forceinline__ void seq_dot4x2(const float4* __restrict__ m4, uint32_t r, const float* v0,
+                                           const float* v1, uint32_t n, float& a0, float& a1) {
+    const float4* col = m4 + r;
     float x0 = 0.0f, x1 = 0.0f;
     uint32_t i = 0;
-    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
-        for (; i + 4 * kDot2Batch <= n; i += 4 * kDot2Batch) {
-            float4 r[kDot2Batch];
+    for (; i + 4 * kDot2Batch <= n; i += 4 * kDot2Batch) {
+        float4 x[kDot2Batch];
 #pragma unroll
-            for (uint32_t b = 0; b < kDot2Batch; ++b) r[b] = *reinterpret_cast<const float4*>(row + i + 4 * b);
+        for (uint32_t b = 0; b < kDot2Batch; ++b) x[b] = col[(size_t)(i / 4 + b) * R];
 #pragma unroll
-            for (uint32_t b = 0; b < kDot2Batch; ++b) {
-                const uint32_t j = i + 4 * b;
-                x0 += r[b].x * v0[j];
-                x1 += r[b].x * v1[j];
-                x0 += r[b].y * v0[j + 1];
-                x1 += r[b].y * v1[j + 1];
-                x0 += r[b].z * v0[j + 2];
-                x1 += r[b].z * v1[j + 2];
-                x0 += r[b].w * v0[j + 3];
-                x1 += r[b].w * v1[j + 3];
-            }
+        for (uint32_t b = 0; b < kDot2Batch; ++b) {
+            const uint32_t j = i + 4 * b;
+            x0 += x[b].x * v0[j];
+            x1 += x[b].x * v1[j];
+            x0 += x[b].y * v0[j + 1];
+            x1 += x[b].y * v1[j + 1];
+            x0 += x[b].z * v0[j + 2];
+            x1 += x[b].z * v1[j + 2];
+            x0 += x[b].w * v0[j + 3];
+            x1 += x[b].w * v1[j + 3];
         }
     }
-    for (; i < n; ++i) {
-        x0 += row[i] * v0[i];
-        x1 += row[i] * v1[i];
+    for (; i < n; i += 4) {
+        const float4 x = col[(size_t)(i / 4) * R];
+        const float e[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c)
+            if (i + c < n) {
+                x0 += e[c] * v0[i + c];
+                x1 += e[c] * v1[i + c];
+            }
     }
     a0 = x0, a1 = x1;
 }
@@ -3010,8 +3024,8 @@ __global__ __launch_bounds__(256, (CODEC == kCodecInt4Single || CODEC == kCodecI
         lds_load_vec(keys, dtype, k0, a.d, key0);
         if (two) lds_load_vec(keys, dtype, k0 + 1, a.d, key1);
         __syncthreads();
-        if (tid < 128) h0[tid] = seq_dot(a.p + (size_t)tid * a.d, key0, a.d);
-        else if (two) h1[tid - 128] = seq_dot(a.p + (size_t)(tid - 128) * a.d, key1, a.d);
+        if (tid < 128) h0[tid] = seq_dot4<128>(a.p4, tid, key0, a.d);
+        else if (two) h1[tid - 128] = seq_dot4<128>(a.p4, tid - 128, key1, a.d);
         __syncthreads();
         for (uint32_t i = tid; i < a.d; i += blockDim.x) {
             float r0 = 0.0f, r1 = 0.0f;
@@ -3035,7 +3049,7 @@ __global__ __launch_bounds__(256, (CODEC == kCodecInt4Single || CODEC == kCodecI
         if (a.diag) block_rht2(buf0, buf1, a.diag, a.d_pad, a.rht_inv);
         {
             float acc0, acc1;
-            seq_dot2(a.z + (size_t)tid * a.d_pad, buf0, buf1, a.d_pad, acc0, acc1);
+            seq_dot4x2<kDS>(a.z4, tid, buf0, buf1, a.d_pad, acc0, acc1);
             const uint64_t m0 = __ballot(acc0 < 0.0f), m1 = __ballot(acc1 < 0.0f);
             if ((tid & 63u) == 0) {
                 misc0[2 * wave] = (uint32_t)m0, misc0[2 * wave + 1] = (uint32_t)(m0 >> 32);
@@ -3084,10 +3098,10 @@ __global__ __launch_bounds__(256) void learned_prepare_kernel(const void* __rest
         lds_load_vec(q, dtype, qi, a.d, vec);
         __syncthreads();
         for (uint32_t i = tid; i < a.d_pad; i += blockDim.x) buf[i] = i < a.d ? vec[i] : 0.0f;
-        if (tid < 128) qc[qi * 128 + tid] = seq_dot(a.p + (size_t)tid * a.d, vec, a.d);
+        if (tid < 128) qc[qi * 128 + tid] = seq_dot4<128>(a.p4, tid, vec, a.d);
         __syncthreads();
         if (a.diag) block_rht(buf, a.diag, a.d_pad, a.rht_inv);
-        block_sign_bits(buf, a.z, a.d_pad, words);
+        block_sign_bits(buf, a.z4, a.d_pad, words);
         __syncthreads();
         if (tid < 4) qs[qi * 4 + tid] = (uint64_t)words[2 * tid] | ((uint64_t)words[2 * tid + 1] << 32);
         __syncthreads();
@@ -3117,13 +3131,13 @@ __global__ __launch_bounds__(256) void learned_prepare2_kernel(const void* __res
             buf0[i] = i < a.d ? vec0[i] : 0.0f;
             buf1[i] = i < a.d && two ? vec1[i] : 0.0f;
         }
-        if (tid < 128) qc[q0 * 128 + tid] = seq_dot(a.p + (size_t)tid * a.d, vec0, a.d);
-        else if (two) qc[(q0 + 1) * 128 + tid - 128] = seq_dot(a.p + (size_t)(tid - 128) * a.d, vec1, a.d);
+        if (tid < 128) qc[q0 * 128 + tid] = seq_dot4<128>(a.p4, tid, vec0, a.d);
+        else if (two) qc[(q0 + 1) * 128 + tid - 128] = seq_dot4<128>(a.p4, tid - 128, vec1, a.d);
         __syncthreads();
         if (a.diag) block_rht2(buf0, buf1, a.diag, a.d_pad, a.rht_inv);
         {
             float acc0, acc1;
-            seq_dot2(a.z + (size_t)tid * a.d_pad, buf0, buf1, a.d_pad, acc0, acc1);
+            seq_dot4x2<kDS>(a.z4, tid, buf0, buf1, a.d_pad, acc0, acc1);
             const uint64_t m0 = __ballot(acc0 < 0.0f), m1 = __ballot(acc1 < 0.0f);
             if ((tid & 63u) == 0) {
                 words[2 * wave] = (uint32_t)m0, words[2 * wave + 1] = (uint32_t)(m0 >> 32);
@@ -4178,7 +4192,8 @@ hipError_t launch_decode(const void* tiles, uint64_t n, const float* z_or_null, 
 
 namespace {
 LearnedArgs learned_args(const LearnedProjection& lp) {
-    return LearnedArgs{lp.p, lp.z, lp.diag, lp.d, lp.d_pad, lp.rht_inv};
+    return LearnedArgs{lp.p, lp.z, lp.diag, reinterpret_cast<const float4*>(lp.p4),
+                       reinterpret_cast<const float4*>(lp.z4), lp.d, lp.d_pad, lp.rht_inv};
 }
 unsigned learned_grid(uint64_t n) { return (unsigned)std::min<uint64_t>(n, 1u << 20); }
 constexpr size_t kLdsMaxBytes = 160 * 1024;  // LDS per workgroup on gfx950

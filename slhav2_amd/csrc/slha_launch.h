@@ -77,6 +77,8 @@ struct LearnedProjection {
     const float* p = nullptr;
     const float* z = nullptr;
     const float* diag = nullptr;
+    const float* p4 = nullptr;  // P interleaved by 4 columns, [ceil(d/4)][128][4]
+    const float* z4 = nullptr;  // Z interleaved by 4 columns, [ceil(d_pad/4)][256][4]
     uint32_t d = 0, d_pad = 0;
     float rht_inv = 1.0f;
 };

@@ -16,7 +16,7 @@ import pytest
 
 import oracle_ffi as o
 
-DEV_CASES = [(192, False), (576, True), (1024, False), (1000, True)]
+DEV_CASES = [(192, False), (576, True), (1024, False), (1000, True), (333, False), (258, True)]
 
 
 @pytest.fixture(scope="module")
