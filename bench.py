@@ -656,7 +656,7 @@ def run_learned(args) -> int:
         warmup, ms, "f32",
         {"workload": "LearnedModel encode on the GPU (learned.rs:353-408, .slhw v2)", "d": d, "d_pad": 1024,
          "keys": n, "key_dtype": "bf16", "codec": "int4", "parallelism": "none (1 GPU)"},
-        roofline=valu_roofline(n * 2.0 * 128 * 4 * d, ms, "slha::learned_encode2_kernel<0>"),
+        roofline=valu_roofline(n * 2.0 * 128 * 4 * d, ms, "slha::learned_encode4_kernel<0>"),
         queries={"queries_per_s": nq / (ms_q * 1e-3), "ms_per_launch": ms_q, "queries": nq},
         decode={"tiles_per_s": n / (ms_d * 1e-3), "ms_per_launch": ms_d, "tiles": n, "with_residual": True})),
         flush=True)
