@@ -3320,70 +3320,97 @@ __global__ __launch_bounds__(256) void learned_prepare2_kernel(const void* __res
 // Tile -> key estimate [d]: reconstruct(dequant_latent) (slha_decode_latent,
 // lib.rs:763-822), plus with_residual the sign-sketch term of
 // reconstruct_from_tile (learned.rs:288-320), omitted for RHT models.
+// kDecTiles tiles per workgroup: every load of P (and Z) feeds their chains,
+// each output its own sequential sum. Tile slots past n are computed on and
+// not stored.
+constexpr uint32_t kDecTiles = 4;
+
 __global__ __launch_bounds__(256) void learned_decode_kernel(const uint4* __restrict__ tiles,
                                                              uint64_t n, LearnedArgs a,
                                                              int with_residual, float sqrt_half_pi,
                                                              float* __restrict__ out) {
+    constexpr uint32_t NT = kDecTiles;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    float* h = lds;
-    uint32_t* misc = reinterpret_cast<uint32_t*>(h + 128);  // residual words 0..7, sigma 8
+    float* hs = lds;                                          // [NT][128]
+    uint32_t* misc = reinterpret_cast<uint32_t*>(hs + NT * 128);  // [NT][32]: residual words 0..7, sigma 8
     __shared__ float cb[16];
     const uint32_t tid = threadIdx.x;
     const bool resid = with_residual && !a.diag;
     stage_codebook(cb);
     __syncthreads();
-    for (uint64_t ti = blockIdx.x; ti < n; ti += gridDim.x) {
-        if (tid < 8) {  // thread g dequantises dims [16g, 16g + 16), operation for operation
+    for (uint64_t t0 = NT * (uint64_t)blockIdx.x; t0 < n; t0 += NT * (uint64_t)gridDim.x) {
+        // thread 8 t + g dequantises dims [16g, 16g + 16) of tile t0 + t,
+        // operation for operation
+        if (tid < 8 * NT && t0 + tid / 8 < n) {
+            const uint32_t t = tid / 8, g = tid % 8;
             uint32_t w[32];
-            load_tile(tiles + ti * 8, w);
+            load_tile(tiles + (t0 + t) * 8, w);
             float k[16];
             switch (codec_class(w[29] >> 16)) {
-                case kClsInt4: decode_group_exact<kClsInt4>(w, (int)tid, cb, k); break;
-                case kClsNF4: decode_group_exact<kClsNF4>(w, (int)tid, cb, k); break;
-                case kClsTQ3: decode_group_exact<kClsTQ3>(w, (int)tid, cb, k); break;
-                case kClsMixed: decode_group_exact<kClsMixed>(w, (int)tid, cb, k); break;
-                default: decode_group_exact<kClsMix3>(w, (int)tid, cb, k); break;
+                case kClsInt4: decode_group_exact<kClsInt4>(w, (int)g, cb, k); break;
+                case kClsNF4: decode_group_exact<kClsNF4>(w, (int)g, cb, k); break;
+                case kClsTQ3: decode_group_exact<kClsTQ3>(w, (int)g, cb, k); break;
+                case kClsMixed: decode_group_exact<kClsMixed>(w, (int)g, cb, k); break;
+                default: decode_group_exact<kClsMix3>(w, (int)g, cb, k); break;
             }
 #pragma unroll
-            for (int j = 0; j < 16; ++j) h[16 * tid + j] = k[j];
-            if (tid == 0) {
-                for (int j = 0; j < 8; ++j) misc[j] = w[16 + j];
-                misc[8] = w[26];
+            for (int j = 0; j < 16; ++j) hs[t * 128 + 16 * g + j] = k[j];
+            if (g == 0) {
+                for (int j = 0; j < 8; ++j) misc[t * 32 + j] = w[16 + j];
+                misc[t * 32 + 8] = w[26];
             }
         }
         __syncthreads();
         // (sigma * sqrt(pi/2)) / 256, learned.rs:303
-        const float sc = __uint_as_float(misc[8]) * sqrt_half_pi / 256.0f;
-        // kDecU outputs per thread side by side (each its own sequential
-        // sum), so every step has kDecU independent loads and adds; lanes
-        // past d compute a clamped copy and do not store.
+        float sc[NT];
+#pragma unroll
+        for (uint32_t t = 0; t < NT; ++t) sc[t] = __uint_as_float(misc[t * 32 + 8]) * sqrt_half_pi / 256.0f;
+        // kDecU outputs per thread and tile side by side (each its own
+        // sequential sum), so every step has kDecU independent loads feeding
+        // NT kDecU adds; lanes past d compute a clamped copy and do not store.
         constexpr uint32_t kDecU = 4;
         for (uint32_t i0 = tid; i0 < a.d; i0 += blockDim.x * kDecU) {
             uint32_t ii[kDecU];
-            float r[kDecU];
+            float r[NT][kDecU];
 #pragma unroll
             for (uint32_t u = 0; u < kDecU; ++u) {
                 const uint32_t i = i0 + u * blockDim.x;
                 ii[u] = i < a.d ? i : a.d - 1u;
-                r[u] = 0.0f;
+#pragma unroll
+                for (uint32_t t = 0; t < NT; ++t) r[t][u] = 0.0f;
             }
             for (uint32_t k = 0; k < 128; ++k) {
-                const float hk = h[k];
                 const float* pk = a.p + (size_t)k * a.d;
+                float pv[kDecU];
 #pragma unroll
-                for (uint32_t u = 0; u < kDecU; ++u) r[u] += hk * pk[ii[u]];
+                for (uint32_t u = 0; u < kDecU; ++u) pv[u] = pk[ii[u]];
+#pragma unroll
+                for (uint32_t t = 0; t < NT; ++t) {
+                    const float hk = hs[t * 128 + k];
+#pragma unroll
+                    for (uint32_t u = 0; u < kDecU; ++u) r[t][u] += hk * pv[u];
+                }
             }
             if (resid) {
                 for (uint32_t s = 0; s < kDS; ++s) {
-                    const float sgn = ((misc[s >> 5] >> (s & 31u)) & 1u) ? -1.0f : 1.0f;
                     const float* zs = a.z + (size_t)s * a.d_pad;
+                    float zv[kDecU];
 #pragma unroll
-                    for (uint32_t u = 0; u < kDecU; ++u) r[u] += sgn * sc * zs[ii[u]];
+                    for (uint32_t u = 0; u < kDecU; ++u) zv[u] = zs[ii[u]];
+#pragma unroll
+                    for (uint32_t t = 0; t < NT; ++t) {
+                        const float sgn = ((misc[t * 32 + (s >> 5)] >> (s & 31u)) & 1u) ? -1.0f : 1.0f;
+#pragma unroll
+                        for (uint32_t u = 0; u < kDecU; ++u) r[t][u] += sgn * sc[t] * zv[u];
+                    }
                 }
             }
 #pragma unroll
-            for (uint32_t u = 0; u < kDecU; ++u)
-                if (i0 + u * blockDim.x < a.d) out[ti * a.d + i0 + u * blockDim.x] = r[u];
+            for (uint32_t t = 0; t < NT; ++t)
+                if (t0 + t < n)
+#pragma unroll
+                    for (uint32_t u = 0; u < kDecU; ++u)
+                        if (i0 + u * blockDim.x < a.d) out[(t0 + t) * a.d + i0 + u * blockDim.x] = r[t][u];
         }
         __syncthreads();
     }
@@ -4440,7 +4467,7 @@ hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const 
 hipError_t launch_learned_decode(const void* tiles, uint64_t n, const LearnedProjection& lp,
                                  int with_residual, float sqrt_half_pi, float* out, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    learned_decode_kernel<<<learned_grid(n), 256, (128 + 32) * 4, s>>>(
+    learned_decode_kernel<<<learned_grid((n + kDecTiles - 1) / kDecTiles), 256, kDecTiles * (128 + 32) * 4, s>>>(
         static_cast<const uint4*>(tiles), n, learned_args(lp), with_residual, sqrt_half_pi, out);
     return hipGetLastError();
 }
