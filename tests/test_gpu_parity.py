@@ -620,6 +620,48 @@ def test_paged_topk(s, torch, const_scores, page_tiles, flag_set, group):
         base += hq * l
 
 
+def test_paged_topk_many_sequences(s, torch):
+    # Eleven ragged sequences (one token to past two segments), 30 % WARM
+    # tiles, mixed INT4/NF4 waves and a tie plateau across a segment edge;
+    # two calls in a row on one stream (the per-stream top-k workspace is
+    # reused), each checked row by row against the oracle.
+    lens = [17000, 1, 300, 40000, 64, 5000, 16384, 999, 20000, 7, 16385]
+    n_kv, group, k, page_tiles = 2, 4, 64, 256
+    hq = n_kv * group
+    for call in range(2):
+        print(f"paged many-sequence call {call}", flush=True)
+        r = np.random.default_rng(31 + call)
+        src = {}
+        for si, l in enumerate(lens):
+            for h in range(n_kv):
+                t = random_tiles(l, 7000 * call + 100 * si + h, [0, 2])
+                for i in np.nonzero(r.random(l) < 0.3)[0]:
+                    t[i:i + 1] = o.page_out(t[i])
+                src[(si, h)] = t
+        # a plateau straddling the first segment edge of sequence 0, head 1
+        q = r.normal(size=(len(lens) * hq, 128)).astype(np.float32)
+        qs = r.integers(0, 2**63, (len(lens) * hq, 4), dtype=np.uint64)
+        t = src[(0, 1)]
+        t[16384 - 20:16384 + 60] = t[16384 - 20]
+        arena, table, max_pages = build_paged(lens, n_kv, page_tiles, 9 + call, src)
+        scores, idx, val = s.gpu_score_paged_topk(
+            dev(torch, arena.view(np.uint8).reshape(-1, 128)), page_tiles, dev(torch, table),
+            max_pages, dev(torch, np.asarray(lens, np.int32)), n_kv, group, dev(torch, q),
+            dev(torch, qs.view(np.int64)), k)
+        scores, idx, val = scores.cpu().numpy(), idx.cpu().numpy().view(np.uint32), val.cpu().numpy()
+        base = 0
+        for si, l in enumerate(lens):
+            for qh in range(hq):
+                h = qh // group
+                got = scores[base + qh * l: base + (qh + 1) * l]
+                ref, _ = o.score(src[(si, h)], q[si * hq + qh], qs[si * hq + qh])
+                assert_tol(got, ref)
+                ti, tv = o.topk(got, k)
+                assert np.array_equal(idx[si, qh], ti), (call, si, qh)
+                assert np.array_equal(val[si, qh].view(np.uint32), tv.view(np.uint32)), (call, si, qh)
+            base += hq * l
+
+
 def test_c1_cpu_reference_config(s, torch):
     # 4096 f32 N(0,1) keys, INT4, one f32 N(0,1) query.
     keys = o.Rng(0x5EED0000).gaussian(4096 * 128).reshape(4096, 128)
