@@ -491,6 +491,15 @@ def run_c5(args) -> int:
          vp(scores.data_ptr()), k, vp(idx.data_ptr()), vp(val.data_ptr()), vp(stream.cuda_stream))
     steps, warmup = min(args.steps, 20), min(args.warmup, 3)
     ms = timed_steps(lambda i: fn(*a), steps, warmup, stream)
+    # every row's top-k values are its k largest scores (torch.topk on the
+    # same scores; the tie order by index is checked against the oracle in
+    # the GPU tests)
+    torch.cuda.synchronize()
+    for si, L in enumerate(lens):
+        rows = scores[int(base[si]): int(base[si]) + hq * L].view(hq, L)
+        want = torch.topk(rows, min(k, L), dim=1).values
+        if not torch.equal(val[si, :, :min(k, L)], want):
+            raise RuntimeError(f"C5: top-{k} of sequence {si} differs from its scores' k largest")
     # the score pass alone (k = 0), to split the time between the two kernels
     a0 = a[:13] + (0,) + a[14:]
     ms_score = timed_steps(lambda i: fn(*a0), steps, warmup, stream)
@@ -523,6 +532,7 @@ def run_c5(args) -> int:
          "parallelism": "none (1 GPU)"},
         roofline=hbm_roofline(nbytes, ms, "slha::score_paged_fast_kernel<4u> + topk_segment_kernel + topk_merge_kernel", "c5"),
         score_only_ms=ms_score, topk_ms=ms - ms_score,
+        topk_checked="every row's top-k values equal torch.topk of its scores",
         score_only_hbm_gbs=(logical_tile_bytes + pairs * 4) / (ms_score * 1e-3) / 1e9, **extra)),
         flush=True)
     return 0
