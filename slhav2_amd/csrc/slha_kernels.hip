@@ -3317,6 +3317,61 @@ __global__ __launch_bounds__(256) void learned_prepare2_kernel(const void* __res
     }
 }
 
+// Four queries per workgroup (learned_prepare2_kernel's steps, each sum in
+// its order): threads 0-127 form the q_coarse of queries 0 and 1, threads
+// 128-255 those of queries 2 and 3, on one load of P each; the sketch
+// threads run the four chains on one load of Z. Query slots past n_q are
+// computed on and not stored.
+__global__ __launch_bounds__(256) void learned_prepare4_kernel(const void* __restrict__ q, int dtype,
+                                                               uint64_t n_q, LearnedArgs a,
+                                                               float* __restrict__ qc,
+                                                               uint64_t* __restrict__ qs) {
+    constexpr uint32_t NQ = 4;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float* vec = lds;                                                // [NQ][d]
+    float* buf = vec + NQ * a.d;                                     // [NQ][d_pad]
+    uint32_t* words = reinterpret_cast<uint32_t*>(buf + NQ * a.d_pad);  // [NQ][8]
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    for (uint64_t q0 = NQ * (uint64_t)blockIdx.x; q0 < n_q; q0 += NQ * (uint64_t)gridDim.x) {
+        const uint32_t nq = n_q - q0 < NQ ? (uint32_t)(n_q - q0) : NQ;  // uniform
+        for (uint32_t j = 0; j < nq; ++j) lds_load_vec(q, dtype, q0 + j, a.d, vec + j * a.d);
+        __syncthreads();
+        for (uint32_t i = tid; i < a.d_pad; i += blockDim.x)
+#pragma unroll
+            for (uint32_t j = 0; j < NQ; ++j) buf[j * a.d_pad + i] = i < a.d ? vec[j * a.d + i] : 0.0f;
+        {
+            const uint32_t half = tid >> 7, k = tid & 127u;  // queries 2 half, 2 half + 1
+            if (2 * half < nq) {
+                float c[2];
+                seq_dot4xm<128, 2, 8>(a.p4, k, vec + 2 * half * a.d, a.d, a.d, c);
+                qc[(q0 + 2 * half) * 128 + k] = c[0];
+                if (2 * half + 1 < nq) qc[(q0 + 2 * half + 1) * 128 + k] = c[1];
+            }
+        }
+        __syncthreads();
+        if (a.diag) block_rht_n(buf, NQ, a.diag, a.d_pad, a.rht_inv);
+        {
+            float acc[NQ];
+            seq_dot4xm<kDS, NQ, 4>(a.z4, tid, buf, a.d_pad, a.d_pad, acc);
+#pragma unroll
+            for (uint32_t j = 0; j < NQ; ++j) {
+                const uint64_t m = __ballot(acc[j] < 0.0f);
+                if (lane == 0) {
+                    words[8 * j + 2 * wave] = (uint32_t)m;
+                    words[8 * j + 2 * wave + 1] = (uint32_t)(m >> 32);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < 4 * nq) {
+            const uint32_t w = tid & 3u, which = tid >> 2;
+            qs[(q0 + which) * 4 + w] =
+                (uint64_t)words[8 * which + 2 * w] | ((uint64_t)words[8 * which + 2 * w + 1] << 32);
+        }
+        __syncthreads();
+    }
+}
+
 // Tile -> key estimate [d]: reconstruct(dequant_latent) (slha_decode_latent,
 // lib.rs:763-822), plus with_residual the sign-sketch term of
 // reconstruct_from_tile (learned.rs:288-320), omitted for RHT models.
@@ -4449,6 +4504,14 @@ hipError_t launch_learned_encode(const void* keys, int dtype, uint64_t n_keys, u
 hipError_t launch_learned_prepare(const void* q, int dtype, uint64_t n_q, const LearnedProjection& lp,
                                   float* qc, uint64_t* qs, hipStream_t s) {
     if (n_q == 0) return hipSuccess;
+    const size_t lds4 = (4 * ((size_t)lp.d + lp.d_pad) + 32) * 4;
+    if (lds4 <= kLdsMaxBytes && n_q >= 4) {  // four queries per workgroup
+        const hipError_t e = allow_lds(learned_prepare4_kernel, lds4);
+        if (e != hipSuccess) return e;
+        learned_prepare4_kernel<<<learned_grid((n_q + 3) / 4), 256, lds4, s>>>(q, dtype, n_q, learned_args(lp),
+                                                                                qc, qs);
+        return hipGetLastError();
+    }
     const size_t lds2 = learned_lds_bytes2(lp.d, lp.d_pad);
     if (lds2 <= kLdsMaxBytes) {  // two queries per workgroup
         const hipError_t e = allow_lds(learned_prepare2_kernel, lds2);
