@@ -87,10 +87,9 @@ int32_t slha_gpu_prepare_queries(const SlhaModel* model, const void* q_dev, int3
  * Replaces slha_score_tiles (slha-c/src/lib.rs:527-585) and
  * GpuScoringPipeline::score_into (slhav2-vram/src/pipeline.rs:177-230).
  * Tiles are assumed valid (as produced by the encoders); use
- * slha_gpu_validate_tiles to check caller-supplied bytes. For 16 < group <= 64
- * in SLHA_SCORE_FAST mode the call stages the queries once per row into a
- * device workspace (36 KiB per row at group 64) that the library allocates per
- * (device, stream) on first use and reuses; calls on one stream are ordered.
+ * slha_gpu_validate_tiles to check caller-supplied bytes. The call allocates
+ * no device memory: for 16 < group <= 64 in SLHA_SCORE_FAST mode each
+ * workgroup stages the row's queries in its own LDS.
  */
 int32_t slha_gpu_score(const SciRustSlhaTile* tiles_dev, size_t n_rows, size_t n_tok,
                        const float* q_coarse_dev, const uint64_t* q_sign_dev, size_t group,
