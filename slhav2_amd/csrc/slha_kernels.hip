@@ -2082,34 +2082,112 @@ __device__ __forceinline__ uint32_t nf4_nearest(float t) {  // nf4.rs:7-18
     return best;
 }
 
-// One TQ3 code + correction bit (tq3.rs:31-46, mix3.rs:44-58).
+// The quantisers' per-dim quotient x / b (b = the group's effective scale),
+// correctly rounded as the reference's division is.
+//
+// FAST: y = RN(1 / b) once per group, then q0 = RN(x y), the remainder
+// r = x - q0 b (exact in one fma) and RN(q0 + r y), which is RN(x / b) by
+// Markstein's theorem (y within half an ulp of 1 / b, q0 within one ulp of
+// x / b, r exact). The remainder is exact when 2^-96 <= b <= 2^96 and
+// |x / b| >= 2^-6, so quantize() takes this path only for such b. Smaller
+// quotients can be an ulp off, which none of the quantisers' roundings or
+// comparisons can see: their boundary nearest to 0 is |t| = 0.0398, the NF4
+// midpoint next to level 0. Three VALU instead of the division's eleven.
+template <bool FAST>
+__device__ __forceinline__ float quot(float x, float b, float y) {
+    if constexpr (FAST) {
+        const float q0 = x * y;
+        const float r = fmaf(-q0, b, x);
+        return fmaf(r, y, q0);
+    } else {
+        return x / b;
+    }
+}
+__device__ __forceinline__ bool quot_fast_ok(float b) { return b >= 0x1p-96f && b <= 0x1p96f; }
+
+// One TQ3 code + correction bit from t = val / eff (tq3.rs:31-46, mix3.rs:44-58).
 __device__ __forceinline__ void tq3_put(uint32_t* lw, int codes_bit0, int corr_bit0, int ld,
-                                        float val, float eff) {
-    const float t = val / eff;
+                                        float t) {
     const uint32_t code = (uint32_t)clampi(rs_i32(roundf(t + 3.5f)), 0, 7);
     put_bits(lw, codes_bit0 + 3 * ld, code);
     const float level = (float)code - 3.5f;
     if (t - level > 0.0f) put_bits(lw, corr_bit0 + ld, 1u);
 }
 
-// Quantise v into (lw, scale, gsw); returns the codec flag.
+// Codes of v for the effective scale of each group (eff[0] alone for the
+// single-scale INT4 codec; eff[0] = the 8-bit section for mixed and MIX3).
+template <int CODEC, bool FAST>
+__device__ __forceinline__ void put_codes(const float* v, const float* eff, uint32_t* lw) {
+    float y[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        if constexpr (FAST) y[g] = 1.0f / eff[g];
+        else y[g] = 0.0f;
+    }
+    if constexpr (CODEC == kCodecInt4Single) {  // int4.rs:9-24
+#pragma unroll
+        for (int d = 0; d < 128; ++d) {
+            const int32_t q = rs_i32(roundf(quot<FAST>(v[d], eff[0], y[0])));
+            put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+        }
+    } else if constexpr (CODEC == kCodecInt4Grouped || CODEC == kCodecNF4 ||
+                         CODEC == kCodecTQ3) {  // int4.rs:52-60, nf4.rs:44-54, tq3.rs:31-46
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+#pragma unroll
+            for (int d = 16 * g; d < 16 * g + 16; ++d) {
+                const float t = quot<FAST>(v[d], eff[g], y[g]);
+                if constexpr (CODEC == kCodecInt4Grouped) {
+                    const int32_t q = rs_i32(roundf(t));
+                    put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+                } else if constexpr (CODEC == kCodecNF4) {
+                    put_bits(lw, 4 * d, nf4_nearest(eff[g] > 0.0f ? rs_clampf(t, -1.0f, 1.0f) : 0.0f));
+                } else {
+                    tq3_put(lw, 0, 384, d, t);
+                }
+            }
+        }
+    } else {  // mixed.rs:38-55, mix3.rs:36-60
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int32_t q = rs_i32(roundf(quot<FAST>(v[d], eff[0], y[0])));
+            put_bits(lw, 8 * d, (uint32_t)(clampi(q, -128, 127) + 128));
+        }
+#pragma unroll
+        for (int g = 0; g < 7; ++g) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int ld = 16 * g + i;
+                const float t = quot<FAST>(v[8 + ld], eff[1 + g], y[1 + g]);
+                if constexpr (CODEC == kCodecMixed) {
+                    const int32_t q = rs_i32(roundf(t));
+                    put_bits(lw, 64 + 4 * ld, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+                } else {
+                    tq3_put(lw, 64, 400, ld, t);
+                }
+            }
+        }
+    }
+}
+
+// Quantise v into (lw, scale, gsw); returns the codec flag. The codes come
+// from the three-operation quotient when every scale of the key is in its
+// range (nearly always), else from the division; both give the same bits.
 template <int CODEC>
 __device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float* scale_out,
                                              uint32_t* gsw) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) lw[i] = 0u;
-    float steps[8];
+    float steps[8], eff[8];
+    float global;
+    uint32_t flag;
     if constexpr (CODEC == kCodecInt4Single) {  // int4.rs:9-24
         const float max_abs = absmax<0, 128>(v);
-        const float scale = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
-#pragma unroll
-        for (int d = 0; d < 128; ++d) {
-            const int32_t q = rs_i32(roundf(v[d] / scale));
-            put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
-        }
+        global = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
         gsw[0] = gsw[1] = 0xFFFFFFFFu;
-        *scale_out = scale;
-        return 0u;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) eff[g] = global;
+        flag = 0u;
     } else if constexpr (CODEC == kCodecInt4Grouped || CODEC == kCodecNF4 ||
                          CODEC == kCodecTQ3) {  // int4.rs:34-63, nf4.rs:23-57, tq3.rs:10-49
 #pragma unroll
@@ -2121,25 +2199,10 @@ __device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float
                        : CODEC == kCodecNF4       ? m
                                                   : m / 3.5f;
         }
-        const float global = group_bytes(steps, gsw);
+        global = group_bytes(steps, gsw);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const float eff = global * (gs_at(gsw, g) / 255.0f);
-#pragma unroll
-            for (int d = 16 * g; d < 16 * g + 16; ++d) {
-                if constexpr (CODEC == kCodecInt4Grouped) {
-                    const int32_t q = rs_i32(roundf(v[d] / eff));
-                    put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
-                } else if constexpr (CODEC == kCodecNF4) {
-                    const float t = eff > 0.0f ? rs_clampf(v[d] / eff, -1.0f, 1.0f) : 0.0f;
-                    put_bits(lw, 4 * d, nf4_nearest(t));
-                } else {
-                    tq3_put(lw, 0, 384, d, v[d], eff);
-                }
-            }
-        }
-        *scale_out = global;
-        return CODEC == kCodecInt4Grouped ? 0u : (CODEC == kCodecNF4 ? kFlagNF4 : kFlagTQ3);
+        for (int g = 0; g < 8; ++g) eff[g] = global * (gs_at(gsw, g) / 255.0f);
+        flag = CODEC == kCodecInt4Grouped ? 0u : (CODEC == kCodecNF4 ? kFlagNF4 : kFlagTQ3);
     } else {  // mixed.rs:13-57, mix3.rs:11-62
         steps[0] = absmax<0, 8>(v) / 127.0f;
 #pragma unroll
@@ -2149,30 +2212,20 @@ __device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float
             for (int d = 8 + 16 * g; d < 24 + 16 * g; ++d) m = fmaxf(m, fabsf(v[d]));
             steps[1 + g] = CODEC == kCodecMixed ? m / 7.0f : m / 3.5f;
         }
-        const float global = group_bytes(steps, gsw);
-        const float eff_hi = global * (gs_at(gsw, 0) / 255.0f);
+        global = group_bytes(steps, gsw);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            const int32_t q = rs_i32(roundf(v[d] / eff_hi));
-            put_bits(lw, 8 * d, (uint32_t)(clampi(q, -128, 127) + 128));
-        }
-#pragma unroll
-        for (int g = 0; g < 7; ++g) {
-            const float eff = global * (gs_at(gsw, 1 + g) / 255.0f);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int ld = 16 * g + i;
-                if constexpr (CODEC == kCodecMixed) {
-                    const int32_t q = rs_i32(roundf(v[8 + ld] / eff));
-                    put_bits(lw, 64 + 4 * ld, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
-                } else {
-                    tq3_put(lw, 64, 400, ld, v[8 + ld], eff);
-                }
-            }
-        }
-        *scale_out = global;
-        return CODEC == kCodecMixed ? kFlagMixed : kFlagMix3;
+        for (int g = 0; g < 8; ++g) eff[g] = global * (gs_at(gsw, g) / 255.0f);
+        flag = CODEC == kCodecMixed ? kFlagMixed : kFlagMix3;
     }
+    bool fast = true;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) fast = fast && quot_fast_ok(eff[g]);
+    if (fast)
+        put_codes<CODEC, true>(v, eff, lw);
+    else
+        put_codes<CODEC, false>(v, eff, lw);
+    *scale_out = global;
+    return flag;
 }
 
 // Exact dequant of dim d for a statically known codec (tile.rs:141-246).
@@ -2301,15 +2354,16 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
     uint32_t bits[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float sigma = 0.0f, lambda = 0.0f;
     if (residual_mode == kResidualR) {
-        bool finite = true;
         double acc = 0.0;
 #pragma unroll
         for (int d = 0; d < kDC; ++d) {
             v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, scale, d);
-            finite = finite && isfinite(v[d]);
             const double x = (double)v[d];
             acc = fma(x, x, acc);  // x*x is exact in f64, so this equals acc + x*x
         }
+        // Every v[d] is finite iff acc is: 128 squares of finite f32 values sum
+        // to at most 2^263, while an inf or NaN v[d] makes acc inf or NaN.
+        const bool finite = isfinite(acc);
         sigma = finite ? (float)sqrt(acc / 128.0) : __uint_as_float(0x7FC00000u);  // metrics.rs:207-226
         lambda = sigma * lambda_c;
         if (diag) rht128(v, diag, rht_inv);
@@ -2429,15 +2483,14 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
             uint32_t lw[16], gsw[2];
             float scale;
             const uint32_t codec_flag = quantize<CODEC>(v, lw, &scale, gsw);
-            bool finite = true;
             double acc = 0.0;
 #pragma unroll
             for (int d = 0; d < kDC; ++d) {
                 v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, scale, d);
-                finite = finite && isfinite(v[d]);
                 const double x = (double)v[d];
                 acc = fma(x, x, acc);
             }
+            const bool finite = isfinite(acc);  // as in encode_kernel
             const float sigma = finite ? (float)sqrt(acc / 128.0) : __uint_as_float(0x7FC00000u);
             if (diag) rht128(v, diag, rht_inv);
             // ||RHT(e)|| = ||e|| up to ~2^-20; the 2^-10 margin covers it and
