@@ -2024,6 +2024,13 @@ __device__ __forceinline__ int32_t rs_i32(float f) {
     asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
     return r;
 }
+// `f.round() as i32` (half away from zero, then the saturating cast):
+// f + copysign(0.5 - 2^-25, f) truncates to round(f) for every f32 (checked
+// over all 2^32 inputs against roundf), and v_cvt_i32_f32 truncates and
+// saturates as rs_i32 does. Two VALU and the convert instead of roundf's five.
+__device__ __forceinline__ int32_t rs_round_i32(float f) {
+    return rs_i32(f + copysignf(0x1.fffffep-2f, f));
+}
 __device__ __forceinline__ uint32_t rs_u8(float f) {  // `f as u8`
     if (isnan(f)) return 0u;
     if (f >= 255.0f) return 255u;
@@ -2068,18 +2075,22 @@ __device__ __forceinline__ void put_bits(uint32_t* lw, int p, uint32_t v) {
     if (sh > 29 && wi + 1 < 16) lw[wi + 1] |= v >> (32 - sh);
 }
 
-__device__ __forceinline__ uint32_t nf4_nearest(float t) {  // nf4.rs:7-18
-    uint32_t best = 0;
-    float best_d = INFINITY;
+// nf4.rs:7-18 scans the 16 levels for the first smallest f32 |t - L_i|.
+// For t in [-1, 1] (the quantiser clamps it there) level i beats level i - 1
+// in that f32 comparison exactly when t >= T_i, and only neighbours can tie,
+// so the scan's index is the number of thresholds at or below t (0 for NaN,
+// as in the scan). T_i is the smallest f32 for which level i wins, found by
+// bisection; the count equals the scan for every f32 in [-1, 1] and every
+// NaN. 15 compares instead of 16 distance updates.
+__device__ __forceinline__ uint32_t nf4_nearest(float t) {
+    constexpr float kT[15] = {-0x1.b51eb6p-1f, -0x1.3fe5c8p-1f, -0x1.eacd9ep-2f, -0x1.7460a8p-2f,
+                              -0x1.0d9e82p-2f, -0x1.5f3b64p-3f, -0x1.5ab9f6p-4f, 0x1p-29f,
+                              0x1.5ab9f8p-4f,  0x1.5f3b66p-3f,  0x1.0d9e84p-2f,  0x1.7460acp-2f,
+                              0x1.eacda0p-2f,  0x1.3fe5cap-1f,  0x1.b51ebap-1f};
+    uint32_t n = 0;
 #pragma unroll
-    for (uint32_t i = 0; i < 16; ++i) {
-        const float dd = fabsf(t - nf4_level(i));
-        if (dd < best_d) {
-            best_d = dd;
-            best = i;
-        }
-    }
-    return best;
+    for (int i = 0; i < 15; ++i) n += t >= kT[i] ? 1u : 0u;
+    return n;
 }
 
 // The quantisers' per-dim quotient x / b (b = the group's effective scale),
@@ -2088,11 +2099,13 @@ __device__ __forceinline__ uint32_t nf4_nearest(float t) {  // nf4.rs:7-18
 // FAST: y = RN(1 / b) once per group, then q0 = RN(x y), the remainder
 // r = x - q0 b (exact in one fma) and RN(q0 + r y), which is RN(x / b) by
 // Markstein's theorem (y within half an ulp of 1 / b, q0 within one ulp of
-// x / b, r exact). The remainder is exact when 2^-96 <= b <= 2^96 and
-// |x / b| >= 2^-6, so quantize() takes this path only for such b. Smaller
-// quotients can be an ulp off, which none of the quantisers' roundings or
-// comparisons can see: their boundary nearest to 0 is |t| = 0.0398, the NF4
-// midpoint next to level 0. Three VALU instead of the division's eleven.
+// x / b, r exact). r is a multiple of ulp(q0) ulp(b) below b ulp(q0) in
+// magnitude, so it is exact once ulp(q0) ulp(b) >= 2^-149: for
+// 2^-71 <= b <= 2^96 that covers every |x / b| >= 2^-32, and quantize()
+// takes this path only for such b. Smaller quotients can be an ulp off,
+// which none of the quantisers can see: the decisions nearest to 0 are
+// TQ3's code at t = -2^-23 and NF4's choice between +-0.0421 at t = 2^-29.
+// Three VALU instead of the division's eleven.
 template <bool FAST>
 __device__ __forceinline__ float quot(float x, float b, float y) {
     if constexpr (FAST) {
@@ -2103,12 +2116,12 @@ __device__ __forceinline__ float quot(float x, float b, float y) {
         return x / b;
     }
 }
-__device__ __forceinline__ bool quot_fast_ok(float b) { return b >= 0x1p-96f && b <= 0x1p96f; }
+__device__ __forceinline__ bool quot_fast_ok(float b) { return b >= 0x1p-71f && b <= 0x1p96f; }
 
 // One TQ3 code + correction bit from t = val / eff (tq3.rs:31-46, mix3.rs:44-58).
 __device__ __forceinline__ void tq3_put(uint32_t* lw, int codes_bit0, int corr_bit0, int ld,
                                         float t) {
-    const uint32_t code = (uint32_t)clampi(rs_i32(roundf(t + 3.5f)), 0, 7);
+    const uint32_t code = (uint32_t)clampi(rs_round_i32(t + 3.5f), 0, 7);
     put_bits(lw, codes_bit0 + 3 * ld, code);
     const float level = (float)code - 3.5f;
     if (t - level > 0.0f) put_bits(lw, corr_bit0 + ld, 1u);
@@ -2127,7 +2140,7 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
     if constexpr (CODEC == kCodecInt4Single) {  // int4.rs:9-24
 #pragma unroll
         for (int d = 0; d < 128; ++d) {
-            const int32_t q = rs_i32(roundf(quot<FAST>(v[d], eff[0], y[0])));
+            const int32_t q = rs_round_i32(quot<FAST>(v[d], eff[0], y[0]));
             put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
         }
     } else if constexpr (CODEC == kCodecInt4Grouped || CODEC == kCodecNF4 ||
@@ -2138,7 +2151,7 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
             for (int d = 16 * g; d < 16 * g + 16; ++d) {
                 const float t = quot<FAST>(v[d], eff[g], y[g]);
                 if constexpr (CODEC == kCodecInt4Grouped) {
-                    const int32_t q = rs_i32(roundf(t));
+                    const int32_t q = rs_round_i32(t);
                     put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
                 } else if constexpr (CODEC == kCodecNF4) {
                     put_bits(lw, 4 * d, nf4_nearest(eff[g] > 0.0f ? rs_clampf(t, -1.0f, 1.0f) : 0.0f));
@@ -2150,7 +2163,7 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
     } else {  // mixed.rs:38-55, mix3.rs:36-60
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            const int32_t q = rs_i32(roundf(quot<FAST>(v[d], eff[0], y[0])));
+            const int32_t q = rs_round_i32(quot<FAST>(v[d], eff[0], y[0]));
             put_bits(lw, 8 * d, (uint32_t)(clampi(q, -128, 127) + 128));
         }
 #pragma unroll
@@ -2160,7 +2173,7 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
                 const int ld = 16 * g + i;
                 const float t = quot<FAST>(v[8 + ld], eff[1 + g], y[1 + g]);
                 if constexpr (CODEC == kCodecMixed) {
-                    const int32_t q = rs_i32(roundf(t));
+                    const int32_t q = rs_round_i32(t);
                     put_bits(lw, 64 + 4 * ld, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
                 } else {
                     tq3_put(lw, 64, 400, ld, t);
