@@ -171,4 +171,4 @@ def test_round_planted_bias_of_one_half_fails():
     """With a bias of exactly 1/2 the largest float below 1/2 would round up."""
     x = np.nextafter(np.float32(0.5), np.float32(0))
     assert np.trunc(np.float32(x + np.float32(0.5))) == 1.0
-    assert np.trunc(np.float32(x + np.float32(0x1.fffffep-2))) == 0.0
+    assert np.trunc(np.float32(x + np.float32(float.fromhex("0x1.fffffep-2")))) == 0.0
