@@ -2421,12 +2421,13 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
 // Layout: one workgroup of 4 waves, one key per lane for the codec part (the
 // same code as encode_kernel), then per wave a 16x16x32 MFMA grid with Z rows
 // as M (16 rows per block sb) and the wave's keys as N (16 per block kb):
-// lane L (c = L%16, g = L/16) supplies row 16sb+c of Z and column 16kb+c of v
-// for dims 32ks+8g..+7 and receives p~ for bits 16sb+4g+r, r = 0..3, of key
-// 16kb+c.
+// lane L (c = L%16, g = L/16) supplies row m = c of row block sb and column
+// 16kb+c of v for dims 32ks+8g..+7, and receives p~ for rows 4g+r, r = 0..3,
+// of key 16kb+c. Row m of block sb is sign bit 32(sb/2) + 8(m/4) + 4(sb%2) +
+// m%4, so the lane's 16 row blocks give byte g of each of the key's 8 words.
 
 constexpr uint32_t kEncQueue = 256;  // queued (key, bit) recomputations per wave
-constexpr uint32_t kEncZAhead = 2;   // Z row blocks in flight ahead of the MFMAs (divides 16)
+constexpr uint32_t kEncZAhead = 2;   // Z row blocks in flight ahead of the MFMAs (divides 8)
 constexpr uint32_t kEncQueueKey = 32;  // keys with more uncertain bits keep them
 
 struct EncWaveLds {
@@ -2532,10 +2533,6 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
         for (uint32_t q = 0; q < 32; ++q)
             *reinterpret_cast<float4*>(enc_chunk(W, lane, q)) =
                 make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-        *reinterpret_cast<uint4*>(&W.bits[lane * 8]) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&W.bits[lane * 8 + 4]) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&W.umask[lane * 8]) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&W.umask[lane * 8 + 4]) = make_uint4(0u, 0u, 0u, 0u);
         W.bound[lane] = full ? INFINITY : bound;
     }
     __syncthreads();
@@ -2559,7 +2556,12 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
         }
     }
     const uint4* zp = zpack + lane;
-    uint32_t wp[4] = {0u, 0u, 0u, 0u}, up[4] = {0u, 0u, 0u, 0u};
+    // Per key block, one funnel shift per projection pushes its sign bit into
+    // sr and its certainty bit into cr; after row blocks 0-7 the registers
+    // move to slo / clo and row blocks 8-15 refill them. Bit
+    // 31 - (4 (sb % 8) + r) then holds row r of row block sb.
+    uint32_t sr[4] = {0u, 0u, 0u, 0u}, slo[4] = {0u, 0u, 0u, 0u};
+    uint32_t cr[4] = {0u, 0u, 0u, 0u}, clo[4] = {0u, 0u, 0u, 0u};
     // Z operands of kEncZAhead row blocks in flight: block sb's 8 loads go
     // out kEncZAhead blocks before it is multiplied, so their L2 latency is
     // covered by that many blocks of MFMAs (the kernel runs one wave per SIMD,
@@ -2608,23 +2610,50 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
                 for (uint32_t o = 0; o < 8; ++o) zr[j][o] = zp[((sb + kEncZAhead) * 8u + o) * 64u];
             }
             __builtin_amdgcn_sched_barrier(0);
+            // Certain: |p~| > bound, i.e. bound - |p~| < 0 (bound >= 2^-100 or
+            // < 0, so a nonzero difference never rounds to 0). A certain p~ is
+            // nonzero, so its sign bit is (p~ < 0); an uncertain one is
+            // recomputed below whatever its bit. NaN differences occur only
+            // for keys whose bits are all recomputed (bound = inf).
 #pragma unroll
-            for (uint32_t kb = 0; kb < 4; ++kb) {
-                uint32_t nib = 0u, u = 0u;
+            for (uint32_t kb = 0; kb < 4; ++kb)
 #pragma unroll
                 for (uint32_t r = 0; r < 4; ++r) {
-                    nib |= (acc[kb][r] < 0.0f ? 1u : 0u) << r;
-                    u |= (fabsf(acc[kb][r]) > bk[kb] ? 0u : 1u) << r;
+                    sr[kb] = __builtin_amdgcn_alignbit(sr[kb], __float_as_uint(acc[kb][r]), 31);
+                    cr[kb] = __builtin_amdgcn_alignbit(
+                        cr[kb], __float_as_uint(bk[kb] - fabsf(acc[kb][r])), 31);
                 }
-                const uint32_t sh = 4u * g + ((sb & 1u) ? 16u : 0u);
-                wp[kb] = ((sb & 1u) ? wp[kb] : 0u) | (nib << sh);
-                up[kb] = ((sb & 1u) ? up[kb] : 0u) | (u << sh);
-                if (sb & 1u) {
-                    const uint32_t w = (16u * kb + c) * 8u + (sb >> 1);
-                    atomicOr(&W.bits[w], wp[kb]);
-                    if (up[kb] != 0u) atomicOr(&W.umask[w], up[kb]);
-                }
+        }
+        if (sb0 + kEncZAhead == 8u) {
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; ++kb) {
+                slo[kb] = sr[kb];
+                clo[kb] = cr[kb];
             }
+        }
+    }
+    // Lane (g, c) holds byte g of every sketch word of key 16 kb + c (the
+    // row order of the Z pack, build_projection_pack): bytes 0-3 of the
+    // bit-reversed slo / clo are words 0-3, those of sr / cr words 4-7. Every
+    // byte of W.bits and W.umask is written here. A key whose residual is all
+    // +-0 (bound < 0) gets bits 0, as every sequential sum is +0; a key with
+    // bound = inf has every bit uncertain.
+    uint8_t* bbytes = reinterpret_cast<uint8_t*>(W.bits);
+    uint8_t* ubytes = reinterpret_cast<uint8_t*>(W.umask);
+#pragma unroll
+    for (uint32_t kb = 0; kb < 4; ++kb) {
+        const bool zero = bk[kb] < 0.0f, full = bk[kb] == INFINITY;
+        const uint32_t s0 = zero ? 0u : __builtin_bitreverse32(slo[kb]);
+        const uint32_t s1 = zero ? 0u : __builtin_bitreverse32(sr[kb]);
+        const uint32_t u0 = full ? 0xFFFFFFFFu : ~__builtin_bitreverse32(clo[kb]);
+        const uint32_t u1 = full ? 0xFFFFFFFFu : ~__builtin_bitreverse32(cr[kb]);
+        const uint32_t o = (16u * kb + c) * 32u + g;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; ++w) {
+            bbytes[o + 4u * w] = (uint8_t)(s0 >> (8u * w));
+            bbytes[o + 16u + 4u * w] = (uint8_t)(s1 >> (8u * w));
+            ubytes[o + 4u * w] = (uint8_t)(u0 >> (8u * w));
+            ubytes[o + 16u + 4u * w] = (uint8_t)(u1 >> (8u * w));
         }
     }
     __syncthreads();
@@ -4443,7 +4472,13 @@ float build_projection_pack(const float* z, void* pack) {
         for (int ks = 0; ks < 4; ++ks)
             for (int lane = 0; lane < 64; ++lane)
                 for (int j = 0; j < 8; ++j) {
-                    const int s = 16 * sb + lane % 16, d = 32 * ks + 8 * (lane / 16) + j;
+                    // Row m of row block sb is Z row 32 (sb / 2) + 8 (m / 4) +
+                    // 4 (sb % 2) + m % 4: the MFMA hands rows 4 g .. 4 g + 3
+                    // to lane group g, so each lane's projections of a key
+                    // fill whole bytes (byte g) of the key's sketch words.
+                    const int m = lane % 16;
+                    const int s = 32 * (sb / 2) + 8 * (m / 4) + 4 * (sb % 2) + m % 4;
+                    const int d = 32 * ks + 8 * (lane / 16) + j;
                     const float x = z[s * kDC + d];
                     const uint16_t hi = bf16_rne(x);
                     const uint16_t mid = bf16_rne(x - bf16_to_float(hi));
