@@ -2129,8 +2129,13 @@ __device__ __forceinline__ void tq3_put(uint32_t* lw, int codes_bit0, int corr_b
 
 // Codes of v for the effective scale of each group (eff[0] alone for the
 // single-scale INT4 codec; eff[0] = the 8-bit section for mixed and MIX3).
-template <int CODEC, bool FAST>
-__device__ __forceinline__ void put_codes(const float* v, const float* eff, uint32_t* lw) {
+// RESID (INT4 codecs): v[d] becomes the residual v[d] - (q - 8 + 8) eff, the
+// same product and difference as v[d] - dequant_dim (group_scale_exact is
+// eff; for the single-scale codec gs = 255 and eff * 1 = eff).
+template <int CODEC, bool FAST, bool RESID>
+__device__ __forceinline__ void put_codes(float* v, const float* eff, uint32_t* lw) {
+    static_assert(!RESID || CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped,
+                  "in-place residual only for the INT4 codecs");
     float y[8];
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
@@ -2140,8 +2145,9 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
     if constexpr (CODEC == kCodecInt4Single) {  // int4.rs:9-24
 #pragma unroll
         for (int d = 0; d < 128; ++d) {
-            const int32_t q = rs_round_i32(quot<FAST>(v[d], eff[0], y[0]));
-            put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+            const int32_t q = clampi(rs_round_i32(quot<FAST>(v[d], eff[0], y[0])), -8, 7);
+            put_bits(lw, 4 * d, (uint32_t)(q + 8) & 0xFu);
+            if constexpr (RESID) v[d] = v[d] - (float)q * eff[0];
         }
     } else if constexpr (CODEC == kCodecInt4Grouped || CODEC == kCodecNF4 ||
                          CODEC == kCodecTQ3) {  // int4.rs:52-60, nf4.rs:44-54, tq3.rs:31-46
@@ -2151,8 +2157,9 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
             for (int d = 16 * g; d < 16 * g + 16; ++d) {
                 const float t = quot<FAST>(v[d], eff[g], y[g]);
                 if constexpr (CODEC == kCodecInt4Grouped) {
-                    const int32_t q = rs_round_i32(t);
-                    put_bits(lw, 4 * d, (uint32_t)(clampi(q, -8, 7) + 8) & 0xFu);
+                    const int32_t q = clampi(rs_round_i32(t), -8, 7);
+                    put_bits(lw, 4 * d, (uint32_t)(q + 8) & 0xFu);
+                    if constexpr (RESID) v[d] = v[d] - (float)q * eff[g];
                 } else if constexpr (CODEC == kCodecNF4) {
                     put_bits(lw, 4 * d, nf4_nearest(eff[g] > 0.0f ? rs_clampf(t, -1.0f, 1.0f) : 0.0f));
                 } else {
@@ -2183,12 +2190,19 @@ __device__ __forceinline__ void put_codes(const float* v, const float* eff, uint
     }
 }
 
+template <int CODEC>
+__device__ __forceinline__ float dequant_dim(const uint32_t* lw, const uint32_t* gsw, float scale,
+                                             int d);
+
 // Quantise v into (lw, scale, gsw); returns the codec flag. The codes come
 // from the three-operation quotient when every scale of the key is in its
 // range (nearly always), else from the division; both give the same bits.
-template <int CODEC>
-__device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float* scale_out,
-                                             uint32_t* gsw) {
+// RESID: v is replaced by the residual v - dequant (tile.rs:141-246), in the
+// code loop for the INT4 codecs and by dequant_dim for the others.
+template <int CODEC, bool RESID>
+__device__ __forceinline__ uint32_t quantize_impl(float* v, uint32_t* lw, float* scale_out,
+                                                  uint32_t* gsw) {
+    constexpr bool kInt4 = CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped;
 #pragma unroll
     for (int i = 0; i < 16; ++i) lw[i] = 0u;
     float steps[8], eff[8];
@@ -2234,11 +2248,20 @@ __device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float
 #pragma unroll
     for (int g = 0; g < 8; ++g) fast = fast && quot_fast_ok(eff[g]);
     if (fast)
-        put_codes<CODEC, true>(v, eff, lw);
+        put_codes<CODEC, true, RESID && kInt4>(v, eff, lw);
     else
-        put_codes<CODEC, false>(v, eff, lw);
+        put_codes<CODEC, false, RESID && kInt4>(v, eff, lw);
+    if constexpr (RESID && !kInt4) {
+#pragma unroll
+        for (int d = 0; d < kDC; ++d) v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, global, d);
+    }
     *scale_out = global;
     return flag;
+}
+template <int CODEC>
+__device__ __forceinline__ uint32_t quantize(const float* v, uint32_t* lw, float* scale_out,
+                                             uint32_t* gsw) {
+    return quantize_impl<CODEC, false>(const_cast<float*>(v), lw, scale_out, gsw);  // v unchanged
 }
 
 // Exact dequant of dim d for a statically known codec (tile.rs:141-246).
@@ -2496,11 +2519,11 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(
             load_vec128(keys, dtype, i, v);
             uint32_t lw[16], gsw[2];
             float scale;
-            const uint32_t codec_flag = quantize<CODEC>(v, lw, &scale, gsw);
+            // v becomes the residual e = key - dequant (mode R)
+            const uint32_t codec_flag = quantize_impl<CODEC, true>(v, lw, &scale, gsw);
             double acc = 0.0;
 #pragma unroll
             for (int d = 0; d < kDC; ++d) {
-                v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, scale, d);
                 const double x = (double)v[d];
                 acc = fma(x, x, acc);
             }
