@@ -4209,24 +4209,46 @@ __device__ __forceinline__ void load_group(const float* scores, const uint8_t* s
     }
 }
 
-__device__ __forceinline__ void soft_add(SoftStat& st, float& flag, float v, float t) {
+// x / t for an exp argument x <= 0: quot<FQ>, except that an overflowing
+// x yt (|x / t| beyond FLT_MAX, where the correction would give NaN) is
+// returned as is; its exp is 0, as that of the division's -inf or -FLT_MAX.
+template <bool FQ>
+__device__ __forceinline__ float exp_arg(float x, float t, float yt) {
+    if constexpr (FQ) {
+        const float q0 = x * yt;
+        return isinf(q0) ? q0 : quot<true>(x, t, yt);
+    } else {
+        return x / t;
+    }
+}
+
+// Online softmax statistics of one slot (ccos.rs:257-300). Both branches of
+// the update take exp of -|v - m| / t ((m - v) / t when v > m, else
+// (v - m) / t: the same magnitude, as IEEE subtraction and division are
+// sign-symmetric), so one exp serves either and the update is two selects
+// instead of a divergent branch. The first finite slot of a thread gives
+// l = 1, as l * e + 1 with l = 0 does. FQ: x / t by exp_arg from
+// yt = RN(1 / t) (the launcher checks t's range), which gives the division's
+// bits for |x / t| >= 2^-32 and, below that, an argument whose exp is 1.0f
+// either way.
+template <bool FQ>
+__device__ __forceinline__ void soft_add(SoftStat& st, float& flag, float v, float t, float yt) {
     if (!isfinite(v)) {
         flag = 1.0f;
         return;
     }
     flag = fmaxf(flag, 0.0f);
-    if (v > st.m) {
-        st.l = (st.m == -INFINITY ? 0.0f : st.l * expf((st.m - v) / t)) + 1.0f;
-        st.m = v;
-    } else {
-        st.l += expf((v - st.m) / t);
-    }
+    const bool first = st.m == -INFINITY, up = v > st.m;
+    const float d = first ? 0.0f : fabsf(v - st.m);
+    const float e = expf(exp_arg<FQ>(-d, t, yt));
+    st.l = up ? (first ? 0.0f : st.l * e) + 1.0f : st.l + e;
+    st.m = up ? v : st.m;
 }
 
-template <bool VEC>
+template <bool VEC, bool FQ>
 __global__ __launch_bounds__(256) void observe_stats_kernel(const float* __restrict__ scores,
                                                             const uint8_t* __restrict__ state, uint64_t n,
-                                                            float t, float* __restrict__ partial) {
+                                                            float t, float yt, float* __restrict__ partial) {
     __shared__ float tmp[2][4];
     SoftStat st = {-INFINITY, 0.0f};
     float flag = -1.0f;
@@ -4245,11 +4267,11 @@ __global__ __launch_bounds__(256) void observe_stats_kernel(const float* __restr
         for (uint32_t u = 0; u < kObsUnroll; ++u)
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u) soft_add(st, flag, x[u][k], t);
+                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u) soft_add<FQ>(st, flag, x[u][k], t, yt);
     }
     if (VEC && blockIdx.x == 0 && threadIdx.x == 0)
         for (uint64_t s = 4 * full; s < n; ++s)
-            if (state[s] != 2) soft_add(st, flag, scores[s], t);
+            if (state[s] != 2) soft_add<FQ>(st, flag, scores[s], t, yt);
     st = block_soft(st, t, tmp);
     flag = block_max_f(flag, tmp[0]);
     if (threadIdx.x == 0) {
@@ -4259,10 +4281,10 @@ __global__ __launch_bounds__(256) void observe_stats_kernel(const float* __restr
     }
 }
 
-template <bool VEC>
+template <bool VEC, bool FQ>
 __global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restrict__ scores,
                                                             const uint8_t* __restrict__ state, uint64_t n,
-                                                            float t, const float* __restrict__ partial,
+                                                            float t, float yt, const float* __restrict__ partial,
                                                             float* __restrict__ importance) {
     __shared__ float tmp[2][4];
     SoftStat st = {-INFINITY, 0.0f};
@@ -4297,7 +4319,8 @@ __global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restr
             if (g >= full) continue;
 #pragma unroll
             for (int k = 0; k < (VEC ? 4 : 1); ++k)
-                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u) im[u][k] += expf((x[u][k] - M) / t) * inv;
+                if (((sb[u] >> (8 * k)) & 0xFFu) != 2u)
+                    im[u][k] += expf(exp_arg<FQ>(x[u][k] - M, t, yt)) * inv;
             if constexpr (VEC)
                 *reinterpret_cast<float4*>(importance + 4 * g) = make_float4(im[u][0], im[u][1], im[u][2], im[u][3]);
             else
@@ -4306,7 +4329,7 @@ __global__ __launch_bounds__(256) void observe_apply_kernel(const float* __restr
     }
     if (VEC && blockIdx.x == 0 && threadIdx.x == 0)
         for (uint64_t s = ObsGroups<VEC>(n).full * 4; s < n; ++s)
-            if (state[s] != 2) importance[s] += expf((scores[s] - M) / t) * inv;
+            if (state[s] != 2) importance[s] += expf(exp_arg<FQ>(scores[s] - M, t, yt)) * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -4818,13 +4841,19 @@ hipError_t launch_observe_scores(const float* scores, const uint8_t* state, uint
     const uint64_t need = (groups + 256 * kObsUnroll - 1) / (256 * kObsUnroll);
     const unsigned blocks = (unsigned)(need == 0 ? 1 : need < kObsBlocks ? need : kObsBlocks);
     const float t = temperature;
+    // The per-slot x / t as quot<true> from one reciprocal when t is in the
+    // range where that equals the division (see quot); else the division.
+    const bool fq = t >= 0x1p-71f && t <= 0x1p96f;
+    const float yt = fq ? 1.0f / t : 0.0f;
+#define SLHA_OBS(V, F)                                                                           \
+    observe_stats_kernel<V, F><<<blocks, 256, 0, s>>>(scores, state, n, t, yt, workspace);        \
+    observe_apply_kernel<V, F><<<blocks, 256, 0, s>>>(scores, state, n, t, yt, workspace, importance)
     if (vec) {
-        observe_stats_kernel<true><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace);
-        observe_apply_kernel<true><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace, importance);
+        if (fq) { SLHA_OBS(true, true); } else { SLHA_OBS(true, false); }
     } else {
-        observe_stats_kernel<false><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace);
-        observe_apply_kernel<false><<<blocks, 256, 0, s>>>(scores, state, n, t, workspace, importance);
+        if (fq) { SLHA_OBS(false, true); } else { SLHA_OBS(false, false); }
     }
+#undef SLHA_OBS
     return hipGetLastError();
 }
 

@@ -259,6 +259,27 @@ def test_observe_scores_matches_oracle(sa, torch, n, offset):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("t,spread", [(1e-20, 1e30), (0.7, 1e30), (1e-25, 1.0), (1e30, 1e3), (1e20, 1e-15)])
+def test_observe_scores_extreme_temperatures_and_spreads(sa, torch, t, spread):
+    """x / t where x yt overflows (spread / t beyond FLT_MAX: every weight but
+    the maximum's is exp(-inf) = 0), temperatures outside the range of the
+    reciprocal quotient (1e-25, 1e30: the division path), and quotients below
+    2^-32 (1e-15 / 1e20: exp 1, uniform weights)."""
+    print(f"ccos observe extreme t={t} spread={spread}", flush=True)
+    n = 2000
+    c = sa.ElasticKvCache(arena(torch, 2048), 1 << 60)
+    c.insert(tiles_of(sa, torch, n, seed=21))
+    live = np.ones(n, np.uint8)
+    r = np.random.default_rng(22)
+    imp = np.zeros(n, np.float32)
+    for _ in range(2):
+        sc = (r.standard_normal(n) * spread).astype(np.float32)
+        c.observe_scores(torch.from_numpy(sc).cuda(), t)
+        imp = o.observe_scores(imp, sc, live, t)
+        np.testing.assert_allclose(c._slots()[2], imp, rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.gpu
 def test_informed_eviction_preserves_sinks_and_heavy_hitters(sa, torch):
     """tests/ccos.rs:309-394."""
     t = tiles_of(sa, torch, 8, seed=50)
