@@ -2119,23 +2119,28 @@ __device__ __forceinline__ float quot(float x, float b, float y) {
 __device__ __forceinline__ bool quot_fast_ok(float b) { return b >= 0x1p-71f && b <= 0x1p96f; }
 
 // One TQ3 code + correction bit from t = val / eff (tq3.rs:31-46, mix3.rs:44-58).
-__device__ __forceinline__ void tq3_put(uint32_t* lw, int codes_bit0, int corr_bit0, int ld,
-                                        float t) {
+// Returns the level the tile decodes to, code - 3.5 +- 0.25 (tile.rs:187-207),
+// in the same f32 operations as tq3_level_exact.
+__device__ __forceinline__ float tq3_put(uint32_t* lw, int codes_bit0, int corr_bit0, int ld,
+                                         float t) {
     const uint32_t code = (uint32_t)clampi(rs_round_i32(t + 3.5f), 0, 7);
     put_bits(lw, codes_bit0 + 3 * ld, code);
     const float level = (float)code - 3.5f;
-    if (t - level > 0.0f) put_bits(lw, corr_bit0 + ld, 1u);
+    const bool corr = t - level > 0.0f;
+    if (corr) put_bits(lw, corr_bit0 + ld, 1u);
+    return level + (corr ? 1.0f : -1.0f) * 0.25f;
 }
 
 // Codes of v for the effective scale of each group (eff[0] alone for the
 // single-scale INT4 codec; eff[0] = the 8-bit section for mixed and MIX3).
-// RESID (INT4 codecs): v[d] becomes the residual v[d] - (q - 8 + 8) eff, the
-// same product and difference as v[d] - dequant_dim (group_scale_exact is
-// eff; for the single-scale codec gs = 255 and eff * 1 = eff).
+// RESID (INT4 codecs and TQ3): v[d] becomes the residual v[d] - level * eff,
+// the same product and difference as v[d] - dequant_dim (group_scale_exact
+// is eff; for the single-scale codec gs = 255 and eff * 1 = eff).
 template <int CODEC, bool FAST, bool RESID>
 __device__ __forceinline__ void put_codes(float* v, const float* eff, uint32_t* lw) {
-    static_assert(!RESID || CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped,
-                  "in-place residual only for the INT4 codecs");
+    static_assert(!RESID || CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped ||
+                      CODEC == kCodecTQ3,
+                  "in-place residual only for the INT4 codecs and TQ3");
     float y[8];
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
@@ -2163,7 +2168,8 @@ __device__ __forceinline__ void put_codes(float* v, const float* eff, uint32_t* 
                 } else if constexpr (CODEC == kCodecNF4) {
                     put_bits(lw, 4 * d, nf4_nearest(eff[g] > 0.0f ? rs_clampf(t, -1.0f, 1.0f) : 0.0f));
                 } else {
-                    tq3_put(lw, 0, 384, d, t);
+                    const float level = tq3_put(lw, 0, 384, d, t);
+                    if constexpr (RESID) v[d] = v[d] - level * eff[g];
                 }
             }
         }
@@ -2198,11 +2204,12 @@ __device__ __forceinline__ float dequant_dim(const uint32_t* lw, const uint32_t*
 // from the three-operation quotient when every scale of the key is in its
 // range (nearly always), else from the division; both give the same bits.
 // RESID: v is replaced by the residual v - dequant (tile.rs:141-246), in the
-// code loop for the INT4 codecs and by dequant_dim for the others.
+// code loop for the INT4 codecs and TQ3 and by dequant_dim for the others.
 template <int CODEC, bool RESID>
 __device__ __forceinline__ uint32_t quantize_impl(float* v, uint32_t* lw, float* scale_out,
                                                   uint32_t* gsw) {
-    constexpr bool kInt4 = CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped;
+    constexpr bool kInPlace =
+        CODEC == kCodecInt4Single || CODEC == kCodecInt4Grouped || CODEC == kCodecTQ3;
 #pragma unroll
     for (int i = 0; i < 16; ++i) lw[i] = 0u;
     float steps[8], eff[8];
@@ -2248,10 +2255,10 @@ __device__ __forceinline__ uint32_t quantize_impl(float* v, uint32_t* lw, float*
 #pragma unroll
     for (int g = 0; g < 8; ++g) fast = fast && quot_fast_ok(eff[g]);
     if (fast)
-        put_codes<CODEC, true, RESID && kInt4>(v, eff, lw);
+        put_codes<CODEC, true, RESID && kInPlace>(v, eff, lw);
     else
-        put_codes<CODEC, false, RESID && kInt4>(v, eff, lw);
-    if constexpr (RESID && !kInt4) {
+        put_codes<CODEC, false, RESID && kInPlace>(v, eff, lw);
+    if constexpr (RESID && !kInPlace) {
 #pragma unroll
         for (int d = 0; d < kDC; ++d) v[d] = v[d] - dequant_dim<CODEC>(lw, gsw, global, d);
     }
