@@ -2458,6 +2458,7 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ ke
 
 constexpr uint32_t kEncQueue = 256;  // queued (key, bit) recomputations per wave
 constexpr uint32_t kEncZAhead = 2;   // Z row blocks in flight ahead of the MFMAs (divides 8)
+static_assert(8u % kEncZAhead == 0u, "the sign registers move to slo / clo after row block 7");
 constexpr uint32_t kEncQueueKey = 32;  // keys with more uncertain bits keep them
 
 struct EncWaveLds {
