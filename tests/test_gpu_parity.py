@@ -159,6 +159,42 @@ def test_encode_sign_fallback_paths(s, torch, rht):
                 raise AssertionError((codec, rht, diff[:10]))
 
 
+def test_encode_small_quotient_boundaries(s, torch):
+    """Quotients x / eff next to the codecs' decisions nearest to 0: NF4
+    chooses between its levels -0.0421 and +0.0421 at t = 2^-29, and TQ3's
+    code flips at t = -2^-23. Each 16-dim group's maximum fixes eff at 1
+    (NF4 step = max, TQ3 step = max / 3.5), then the keys are scaled by
+    powers of two so that eff is 2^-60 (inside the range of the reciprocal
+    quotient) and 2^-80 (outside it: the division). Tile bytes equal the
+    oracle's."""
+    print("encode small quotients", flush=True)
+    r = np.random.default_rng(41)
+
+    def keys_near(t0, top, n):
+        ulps = r.integers(-3, 4, size=(n, 128))
+        base = np.full((n, 128), np.float32(t0))
+        k = base.view(np.int32) + ulps.astype(np.int32)
+        k = k.view(np.float32) * np.where(r.random((n, 128)) < 0.5, 1, -1).astype(np.float32)
+        k[:, ::16] = np.float32(top)  # each group's maximum
+        k[r.random((n, 128)) < 0.1] = 0.0
+        k[:, ::16] = np.float32(top)
+        return k.astype(np.float32)
+
+    with s.Model(seed=43, rht=False) as m:
+        z, _ = m.projection()
+        for codec, t0, top in ((2, 2.0 ** -29, 1.0), (4, -(2.0 ** -23), 3.5), (2, 2.0 ** -32, 1.0),
+                               (4, 2.0 ** -30, 3.5)):
+            base = keys_near(t0, top, 192)
+            for scale in (1.0, 2.0 ** -60, 2.0 ** -80):
+                keys = (base * np.float32(scale)).astype(np.float32)
+                got = tiles_np(s.gpu_encode(m, dev(torch, keys), codec))
+                ref = o.encode(keys, codec, 1, z, None)
+                if got.tobytes() != ref.tobytes():
+                    g = got.view(np.uint8).reshape(-1, 128)
+                    rr = ref.view(np.uint8).reshape(-1, 128)
+                    raise AssertionError((codec, t0, scale, np.nonzero((g != rr).any(1))[0][:10]))
+
+
 def boundary_keys(n, seed):
     """Keys whose elements sit on, or one or two ulps from, the codecs'
     rounding boundaries: with max |k| = 7 (INT4 step 1) every half-integer
