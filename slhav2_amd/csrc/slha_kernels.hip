@@ -4153,7 +4153,7 @@ __global__ __launch_bounds__(256) void tile_scatter_kernel(const uint4* __restri
 //      importance of each live slot.
 // L differs from the reference's sequential sum by rounding only (relative
 // error a few f32 ulps). partial holds 3 * kObsBlocks floats.
-constexpr uint32_t kObsBlocks = 1024, kObsUnroll = 4;
+constexpr uint32_t kObsBlocks = 512, kObsUnroll = 4;
 
 struct SoftStat {
     float m, l;
