@@ -4366,10 +4366,11 @@ hipError_t launch_score_rows(const void* tiles, uint32_t n_rows, uint32_t n_tok,
         else if (n_tok >= kWideMaxTok)
             score_rows_kernel<false, false><<<grid, 256, smem, s>>>(tp, n_tok, group, qc, qsw, scores, ham);
         else {
-            // resident workgroups: about two per CU over all rows, each
-            // looping over its row's 512-tile chunks
+            // about four workgroups per CU over all rows (two resident at a
+            // time), each looping over its row's 512-tile chunks; a
+            // same-box sweep put 1 024 workgroups ahead of 512 and 2 048
             const uint32_t n_chunks = (n_tok + kWideChunk - 1) / kWideChunk;
-            const uint32_t per_row = std::max(1u, std::min(n_chunks, (512u + n_rows - 1) / n_rows));
+            const uint32_t per_row = std::max(1u, std::min(n_chunks, (1024u + n_rows - 1) / n_rows));
             const dim3 wgrid(per_row, n_rows);
             if (group <= 32)
                 score_rows_wide_kernel<1><<<wgrid, 512, wide_image_bytes(group), s>>>(tp, n_tok, group, qc,
