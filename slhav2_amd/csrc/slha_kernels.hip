@@ -4057,21 +4057,41 @@ __global__ __launch_bounds__(256) void eventlog_pack_kernel(const uint4* __restr
                                                             uint64_t n, uint32_t version,
                                                             uint4* __restrict__ records) {
     __shared__ uint4 rec[256 * kRecordQuads];
+    __shared__ uint32_t s_slot[256];
     const uint64_t base = (uint64_t)blockIdx.x * 256u;
     const uint32_t tid = threadIdx.x;
     const uint32_t cnt = n - base < 256u ? (uint32_t)(n - base) : 256u;
+    uint64_t seq = 0;
+    uint32_t slot = 0;
     if (tid < cnt) {
-        const uint64_t seq = seqs[base + tid];
-        const uint32_t slot = slots[base + tid];
+        seq = seqs[base + tid];
+        slot = slots[base + tid];
+        s_slot[tid] = slot;
+    }
+    __syncthreads();
+    // Tiles enter with 8 lanes per tile (lane quad tid % 8 of tile
+    // tid / 8 + 32 k), so each load instruction reads whole 128-byte lines
+    // rather than 16 bytes of 64 scattered tiles; thread r then checksums
+    // record r from LDS.
+    uint4 q[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t r = (tid >> 3) + 32u * k;
+        q[k] = r < cnt ? arena[(size_t)s_slot[r] * 8 + (tid & 7u)] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t r = (tid >> 3) + 32u * k;
+        if (r < cnt) rec[r * kRecordQuads + 1u + (tid & 7u)] = q[k];
+    }
+    __syncthreads();
+    if (tid < cnt) {
         uint4 t[8];
-        const uint4* src = arena + (size_t)slot * 8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = src[j];
-        const uint32_t ck = version >= 2 ? record_checksum(seq, slot, t) : 0u;
         uint4* r = rec + tid * kRecordQuads;
-        r[0] = make_uint4((uint32_t)seq, (uint32_t)(seq >> 32), slot, ck);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[1 + j] = t[j];
+        for (int j = 0; j < 8; ++j) t[j] = r[1 + j];
+        const uint32_t ck = version >= 2 ? record_checksum(seq, slot, t) : 0u;
+        r[0] = make_uint4((uint32_t)seq, (uint32_t)(seq >> 32), slot, ck);
     }
     __syncthreads();
     uint4* out = records + base * kRecordQuads;
